@@ -1,0 +1,124 @@
+// Drop-in C++ declarations of the fused per-layer ops, with the signatures of the reference engine's src/ops.h
+// (namespace q27, same names, parameter order and defaults; cudaStream_t becomes hipStream_t). Each function
+// forwards to the C ABI of include/q27h.h and throws std::runtime_error on a non-zero status, as the reference
+// launchers throw on bad shapes (src/ops.cu:699,704,724,734) and through CK (src/common.cuh:11-12).
+// Only the functions of the fused-op path are declared; the GEMV, attention and delta-rule kernels of src/ops.h
+// are outside this library.
+#pragma once
+#include <hip/hip_bf16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "../q27h.h"
+
+namespace q27 {
+
+inline void q27h_check(int status) {
+  if (status != Q27H_OK) throw std::runtime_error(std::string("q27h: ") + q27h_last_error());
+}
+
+// src/ops.h:15
+inline void rmsnorm(const float* x, const float* w, float* y, int n, int rows, float eps, hipStream_t s, int ystride = 0) {
+  q27h_check(q27h_rmsnorm(x, w, y, n, rows, eps, s, ystride));
+}
+// src/ops.h:17
+inline void add(const float* x, const float* a, float* y, int n, hipStream_t s) { q27h_check(q27h_add(x, a, y, n, s)); }
+// src/ops.h:19
+inline void swiglu(const float* g, const float* u, float* y, int n, hipStream_t s) { q27h_check(q27h_swiglu(g, u, y, n, s)); }
+// src/ops.h:22-23
+inline void get_rows_iq2_s(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, hipStream_t s,
+                           const float* img = nullptr) {
+  q27h_check(q27h_get_rows_iq2_s(table, row_bytes, ids, T, y, n, s, img));
+}
+// Same signature for the ggml K-quant / Q8_0 tables (no reference counterpart: its embedding is IQ2_S only).
+inline void get_rows_q4_k(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, hipStream_t s,
+                          const float* img = nullptr) {
+  q27h_check(q27h_get_rows_q4_k(table, row_bytes, ids, T, y, n, s, img));
+}
+inline void get_rows_q6_k(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, hipStream_t s,
+                          const float* img = nullptr) {
+  q27h_check(q27h_get_rows_q6_k(table, row_bytes, ids, T, y, n, s, img));
+}
+inline void get_rows_q8_0(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, hipStream_t s,
+                          const float* img = nullptr) {
+  q27h_check(q27h_get_rows_q8_0(table, row_bytes, ids, T, y, n, s, img));
+}
+// src/ops.h:29-30
+inline void gdn_gates(const float* a, const float* b, const float* ssm_a, const float* dt_bias, float* g, float* beta, int H,
+                      int T, hipStream_t s) {
+  q27h_check(q27h_gdn_gates(a, b, ssm_a, dt_bias, g, beta, H, T, s));
+}
+// src/ops.h:32-33
+inline void gdn_conv(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,
+                     bool snapshots, hipStream_t s) {
+  q27h_check(q27h_gdn_conv(x, w, planes, in_plane, y, C, T, snapshots ? 1 : 0, s));
+}
+// src/ops.h:36
+inline void l2norm_heads(float* x, int n, int heads, int T, int stride, float eps, hipStream_t s) {
+  q27h_check(q27h_l2norm_heads(x, n, heads, T, stride, eps, s));
+}
+// src/ops.h:43
+inline void gated_rmsnorm(const float* o, const float* w, const float* z, float* y, int n, int heads, float eps,
+                          hipStream_t s) {
+  q27h_check(q27h_gated_rmsnorm(o, w, z, y, n, heads, eps, s));
+}
+// src/ops.h:44
+inline void set_int(int* p, int v, hipStream_t s) { q27h_check(q27h_set_int(p, v, s)); }
+// src/ops.h:54
+inline size_t kv_cache_bytes(int nkvh, int n_ctx, bool q8) { return q27h_kv_cache_bytes(nkvh, n_ctx, q8 ? 1 : 0); }
+// src/ops.h:59-62
+inline void attn_prep(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm, float* qn,
+                      void* kcache, void* vcache, const int* pos0, int T, float eps, float theta_scale, int nqh, int nkvh,
+                      int n_ctx, bool q8, hipStream_t s, const void* pf = nullptr, size_t pf_bytes = 0,
+                      const int* rope3 = nullptr, const int* rdelta = nullptr) {
+  q27h_check(q27h_attn_prep(qg, k, v, q_norm, k_norm, qn, kcache, vcache, pos0, T, eps, theta_scale, nqh, nkvh, n_ctx,
+                            q8 ? 1 : 0, s, pf, pf_bytes, rope3, rdelta));
+}
+
+// src/ops.h:81-97: the two-card exchange arguments. Accepted for source compatibility; a non-null ArArgs* makes
+// sum_norm_q8 throw (this library runs one GPU, tensor parallelism is outside it).
+struct ArArgs {
+  __hip_bfloat16* host_mine = nullptr;
+  const __hip_bfloat16* host_other = nullptr;
+  int* flag_mine = nullptr;
+  const int* flag_other = nullptr;
+  const int* dstep = nullptr;
+  int n_ar = 0, index = 0;
+  int* err = nullptr;
+  float* ef = nullptr;
+  int ef_first = 1;
+  unsigned long long* tprof = nullptr;
+};
+
+// src/ops.h:99-100
+inline void rmsnorm_q8(const float* x, const float* w, float* h, int8_t* xq, float* xd, int n, int rows, float eps,
+                       hipStream_t s, float* xs = nullptr) {
+  q27h_check(q27h_rmsnorm_q8(x, w, h, xq, xd, n, rows, eps, s, xs));
+}
+// src/ops.h:103-104
+inline void sum_norm_q8(float* x, const float* partial, int n, int rows, const ArArgs* ar, const float* w, float eps, float* h,
+                        int8_t* xq, float* xd, hipStream_t s, const void* pf = nullptr, size_t pf_bytes = 0) {
+  q27h_check(q27h_sum_norm_q8(x, partial, n, rows, ar, w, eps, h, xq, xd, s, pf, pf_bytes));
+}
+// src/ops.h:106
+inline void swiglu_q8(const float* g, const float* u, int8_t* xq, float* xd, int n, hipStream_t s, float* xs = nullptr) {
+  q27h_check(q27h_swiglu_q8(g, u, xq, xd, n, s, xs));
+}
+// src/ops.h:108-109
+inline void gated_rmsnorm_q8(const float* o, const float* w, const float* z, int8_t* xq, float* xd, int heads, float eps,
+                             hipStream_t s, float* xs = nullptr) {
+  q27h_check(q27h_gated_rmsnorm_q8(o, w, z, xq, xd, heads, eps, s, xs));
+}
+// src/ops.h:112-114
+inline void gdn_conv_l2(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,
+                        bool snapshots, int n_norm_heads, float eps, const float* a, const float* b, const float* ssm_a,
+                        const float* dt_bias, float* g, float* beta, int H, hipStream_t s, const void* pf = nullptr,
+                        size_t pf_bytes = 0) {
+  q27h_check(q27h_gdn_conv_l2(x, w, planes, in_plane, y, C, T, snapshots ? 1 : 0, n_norm_heads, eps, a, b, ssm_a, dt_bias, g,
+                              beta, H, s, pf, pf_bytes));
+}
+
+}  // namespace q27

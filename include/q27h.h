@@ -1,0 +1,139 @@
+/* q27h: C ABI of the MI355X (gfx950) fused per-layer ops of the qwen27 engine.
+ *
+ * Every entry point mirrors one launcher of the reference engine (avallavall/qwen27-engine) with the same
+ * argument order and meaning, plain device pointers and an opaque stream (`q27h_stream_t` is a hipStream_t;
+ * NULL = the default stream). Each call only enqueues work on that stream and returns; nothing synchronises
+ * the host, and device-resident scalars (positions, plane index, ids) are read on the device, so every call
+ * may be recorded in a HIP graph. Return value: Q27H_OK, or a negative code with q27h_last_error() holding
+ * the message (per host thread). The C++ header q27/ops.h re-exposes the reference's exact signatures on
+ * top of these and throws std::runtime_error on a non-zero status.
+ *
+ * Layout rules shared by all entry points: rows are contiguous ([rows][n]); float arrays read or written four
+ * values at a time must be 16-byte aligned (any row offset of a 5120-wide or 128-wide array keeps this);
+ * q8_1 outputs are xq int8 [..][K], xd f32 [..][K/32] (the value of the fp16-rounded scale) and the optional
+ * xs f32 [..][K/16] (sums of the unquantized values per 16).
+ */
+#ifndef Q27H_H
+#define Q27H_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q27H_ABI_VERSION 1
+
+#define Q27H_OK 0
+#define Q27H_ERR_SHAPE (-1)       /* a size the reference launcher rejects (std::runtime_error there) */
+#define Q27H_ERR_UNSUPPORTED (-2) /* a feature outside this build: the two-GPU exchange arguments */
+#define Q27H_ERR_HIP (-3)         /* a HIP runtime error at launch */
+#define Q27H_ERR_ARG (-4)         /* null or misaligned pointer */
+
+typedef void* q27h_stream_t;
+
+const char* q27h_last_error(void);
+int q27h_abi_version(void);
+
+/* ---------------------------------------------------------------- element-wise and unfused norms */
+/* rmsnorm (src/ops.h:15, src/ops.cu:746-748): y = x * rsqrt(mean(x^2) + eps) * w per row; ystride 0 = n. */
+int q27h_rmsnorm(const float* x, const float* w, float* y, int n, int rows, float eps, q27h_stream_t s, int ystride);
+/* add (src/ops.h:17, src/ops.cu:749-751): y = x + a over n values. */
+int q27h_add(const float* x, const float* a, float* y, int n, q27h_stream_t s);
+/* swiglu (src/ops.h:19, src/ops.cu:752-754): y = silu(g) * u over n values. */
+int q27h_swiglu(const float* g, const float* u, float* y, int n, q27h_stream_t s);
+/* set_int (src/ops.h:45, src/ops.cu:744): *p = v, enqueued. */
+int q27h_set_int(int* p, int v, q27h_stream_t s);
+
+/* ---------------------------------------------------------------- q8_1 producers (fused) */
+/* rmsnorm_q8 (src/ops.h:99-100, src/ops.cu:697-701): RMSNorm of `rows` rows of n = 5120 -> h (may be NULL),
+ * q8_1 xq/xd and xs (may be NULL). */
+int q27h_rmsnorm_q8(const float* x, const float* w, float* h, int8_t* xq, float* xd, int n, int rows, float eps,
+                    q27h_stream_t s, float* xs);
+/* sum_norm_q8 (src/ops.h:103-104, src/ops.cu:702-722): x += partial in place, then rmsnorm_q8 of x (no xs).
+ * `ar` is the reference's two-card ArArgs: must be NULL here (Q27H_ERR_UNSUPPORTED otherwise). pf/pf_bytes
+ * (an L2 prefetch hint of the next GEMV's weights) are accepted and ignored. n must be 5120. */
+int q27h_sum_norm_q8(float* x, const float* partial, int n, int rows, const void* ar, const float* w, float eps, float* h,
+                     int8_t* xq, float* xd, q27h_stream_t s, const void* pf, size_t pf_bytes);
+/* sum_norm_rows (src/prefill.h:31-32, src/prefill.cu:489-501): prefill form of sum_norm_q8 with xs; `ex` (the
+ * reference's PfExchange) must be NULL. */
+int q27h_sum_norm_rows(float* x, const float* partial, int n, int M, const void* ex, const float* w, float eps, float* h,
+                       int8_t* xq, float* xd, float* xs, q27h_stream_t s);
+/* add_norm_rows (src/prefill.h:46-47, src/prefill.cu:516-520): x += partial (recv NULL) or
+ * x += bf16(partial) + recv (recv = bf16 bits [M][n]), then RMSNorm -> h (may be NULL), q8_1 and xs. */
+int q27h_add_norm_rows(float* x, const float* partial, const uint16_t* recv, int n, int M, const float* w, float eps,
+                       float* h, int8_t* xq, float* xd, float* xs, q27h_stream_t s);
+/* quantize_q8_1 (src/qmat.h:50, src/qgemv.cu:840-845): x[ncols][K] -> q8_1 (+ xs). K % 32 == 0. */
+int q27h_quantize_q8_1(const float* x, int8_t* xq, float* xd, int K, int ncols, q27h_stream_t s, float* xs);
+/* swiglu_q8 (src/ops.h:106, src/ops.cu:723-726): silu(g) * u -> q8_1 (+ xs) over n values, n % 32 == 0. */
+int q27h_swiglu_q8(const float* g, const float* u, int8_t* xq, float* xd, int n, q27h_stream_t s, float* xs);
+/* gated_rmsnorm_q8 (src/ops.h:108-109, src/ops.cu:727-730): per head of 128,
+ * (rms_norm(o) * w) * silu(z) -> q8_1 (+ xs), `heads` heads (tokens x value heads). */
+int q27h_gated_rmsnorm_q8(const float* o, const float* w, const float* z, int8_t* xq, float* xd, int heads, float eps,
+                          q27h_stream_t s, float* xs);
+/* gated_rmsnorm (src/ops.h:43, src/ops.cu:794-796): the unfused form, y = (rms_norm_n(o) * w) * silu(z). */
+int q27h_gated_rmsnorm(const float* o, const float* w, const float* z, float* y, int n, int heads, float eps,
+                       q27h_stream_t s);
+
+/* ---------------------------------------------------------------- Gated-DeltaNet input stage */
+/* l2norm_heads (src/ops.h:34, src/ops.cu:781-783): x <- rms_norm(x, eps/n) / sqrt(n) per head of n values;
+ * `heads` heads at the start of each of T rows of `stride` values. In place. */
+int q27h_l2norm_heads(float* x, int n, int heads, int T, int stride, float eps, q27h_stream_t s);
+/* gdn_gates (src/ops.h:29-30, src/ops.cu:773-776): beta = sigmoid(b), g = softplus(a + dt_bias) * ssm_a, [T][H]. */
+int q27h_gdn_gates(const float* a, const float* b, const float* ssm_a, const float* dt_bias, float* g, float* beta, int H,
+                   int T, q27h_stream_t s);
+/* gdn_conv (src/ops.h:32-33, src/ops.cu:777-780): 4-tap causal conv + SiLU over C channels and T <= 4 tokens;
+ * planes [4][C][3]; *in_plane (device) selects the input state. */
+int q27h_gdn_conv(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T, int snapshots,
+                  q27h_stream_t s);
+/* gdn_conv_l2 (src/ops.h:112-114, src/ops.cu:731-737): gdn_conv + l2norm_heads of the first n_norm_heads heads
+ * + gdn_gates in one launch. C % 128 == 0 and C / 128 - n_norm_heads == H. pf/pf_bytes ignored. */
+int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,
+                     int snapshots, int n_norm_heads, float eps, const float* a, const float* b, const float* ssm_a,
+                     const float* dt_bias, float* g, float* beta, int H, q27h_stream_t s, const void* pf, size_t pf_bytes);
+/* gdn_conv_prefill (src/prefill.h:14-16, src/prefill.cu:479-485): the same over M tokens; the conv state after
+ * the batch goes to plane (*in_plane == 0 ? 1 : 0). */
+int q27h_gdn_conv_prefill(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int M,
+                          int n_norm_heads, float eps, const float* a, const float* b, const float* ssm_a,
+                          const float* dt_bias, float* g, float* beta, int H, q27h_stream_t s);
+/* gdn_flip_plane (src/prefill.h:18, src/prefill.cu:487): *plane = (*plane == 0 ? 1 : 0), enqueued. */
+int q27h_gdn_flip_plane(int* plane, q27h_stream_t s);
+/* flip_plane_to (src/prefill.h:41, src/prefill.cu:515): *dst = (*src == 0 ? 1 : 0), enqueued. */
+int q27h_flip_plane_to(int* dst, const int* src, q27h_stream_t s);
+
+/* ---------------------------------------------------------------- attention input stage */
+/* kv_cache_bytes (src/ops.h:54, src/attn.cu:890-892): bytes of one layer's K (or V) cache:
+ * q8 ? nkvh * n_ctx * (256 + 16) : nkvh * n_ctx * 512. */
+size_t q27h_kv_cache_bytes(int nkvh, int n_ctx, int q8);
+/* attn_prep (src/ops.h:59-62, src/ops.cu:798-803): per-head RMSNorm of q (nqh heads at stride 512 of qg) and k
+ * (nkvh heads), NeoX RoPE of dims (j, j + 32), j < 32, with theta = p * theta_scale^j, p = rope3[t][j % 3]
+ * (IMRoPE, rope3 [T][3] device, may be NULL) or *pos0 + t - *rdelta (rdelta may be NULL); qn [T][nqh][256];
+ * K and V to cache row *pos0 + t: f16 [nkvh][n_ctx][256] (q8 = 0) or q8_0 int8 [nkvh][n_ctx][256] followed by
+ * fp16 scales [nkvh][n_ctx][8]. Rows outside [0, n_ctx) are not written. pf/pf_bytes ignored. */
+int q27h_attn_prep(const float* qg, const float* k, const float* v, const float* q_norm, const float* k_norm, float* qn,
+                   void* kcache, void* vcache, const int* pos0, int T, float eps, float theta_scale, int nqh, int nkvh,
+                   int n_ctx, int q8, q27h_stream_t s, const void* pf, size_t pf_bytes, const int* rope3,
+                   const int* rdelta);
+
+/* ---------------------------------------------------------------- quantized embedding gather */
+/* get_rows_iq2_s (src/ops.h:22-23, src/ops.cu:756-766): rows ids[t] (device) of an IQ2_S table (82-byte
+ * super-blocks, row_bytes apart) -> f32 y [T][n], n % 256 == 0; id < 0 copies row (-id - 1) of img [..][n]
+ * (zeros when img is NULL). */
+int q27h_get_rows_iq2_s(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, q27h_stream_t s,
+                        const float* img);
+/* No reference kernel (the reference's embedding is IQ2_S only, src/model.cu:104-105); same signature and
+ * id rule as get_rows_iq2_s, ggml block formats: Q4_K (144-byte super-blocks, ggml dequantize_row_q4_K as
+ * transcribed in src/requant.cpp:90-114), Q6_K (210 bytes, src/requant.cpp:68-88), Q8_0 (34-byte blocks of
+ * 32, y = q * fp16 d; n % 32 == 0). */
+int q27h_get_rows_q4_k(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, q27h_stream_t s,
+                       const float* img);
+int q27h_get_rows_q6_k(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, q27h_stream_t s,
+                       const float* img);
+int q27h_get_rows_q8_0(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, q27h_stream_t s,
+                       const float* img);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

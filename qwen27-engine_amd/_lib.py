@@ -1,0 +1,80 @@
+"""Loading and building lib/libq27h.so, and the ctypes signatures of every C-ABI entry point."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libq27h.so")
+
+
+class Q27Error(RuntimeError):
+    """A non-zero status of a q27h_* call; .code is the Q27H_ERR_* value."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{msg} (status {code})")
+        self.code = code
+
+
+_p, _i, _f, _sz, _i64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_int64
+
+# name -> argument types (all return int status unless listed in _RESTYPE)
+SIGNATURES = {
+    "q27h_rmsnorm": [_p, _p, _p, _i, _i, _f, _p, _i],
+    "q27h_add": [_p, _p, _p, _i, _p],
+    "q27h_swiglu": [_p, _p, _p, _i, _p],
+    "q27h_set_int": [_p, _i, _p],
+    "q27h_rmsnorm_q8": [_p, _p, _p, _p, _p, _i, _i, _f, _p, _p],
+    "q27h_sum_norm_q8": [_p, _p, _i, _i, _p, _p, _f, _p, _p, _p, _p, _p, _sz],
+    "q27h_sum_norm_rows": [_p, _p, _i, _i, _p, _p, _f, _p, _p, _p, _p, _p],
+    "q27h_add_norm_rows": [_p, _p, _p, _i, _i, _p, _f, _p, _p, _p, _p, _p],
+    "q27h_quantize_q8_1": [_p, _p, _p, _i, _i, _p, _p],
+    "q27h_swiglu_q8": [_p, _p, _p, _p, _i, _p, _p],
+    "q27h_gated_rmsnorm_q8": [_p, _p, _p, _p, _p, _i, _f, _p, _p],
+    "q27h_gated_rmsnorm": [_p, _p, _p, _p, _i, _i, _f, _p],
+    "q27h_l2norm_heads": [_p, _i, _i, _i, _i, _f, _p],
+    "q27h_gdn_gates": [_p, _p, _p, _p, _p, _p, _i, _i, _p],
+    "q27h_gdn_conv": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
+    "q27h_gdn_conv_l2": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _p, _p, _p, _p, _p, _p, _i, _p, _p, _sz],
+    "q27h_gdn_conv_prefill": [_p, _p, _p, _p, _p, _i, _i, _i, _f, _p, _p, _p, _p, _p, _p, _i, _p],
+    "q27h_gdn_flip_plane": [_p, _p],
+    "q27h_flip_plane_to": [_p, _p, _p],
+    "q27h_kv_cache_bytes": [_i, _i, _i],
+    "q27h_attn_prep": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _f, _f, _i, _i, _i, _i, _p, _p, _sz, _p, _p],
+    "q27h_get_rows_iq2_s": [_p, _i64, _p, _i, _p, _i, _p, _p],
+    "q27h_get_rows_q4_k": [_p, _i64, _p, _i, _p, _i, _p, _p],
+    "q27h_get_rows_q6_k": [_p, _i64, _p, _i, _p, _i, _p, _p],
+    "q27h_get_rows_q8_0": [_p, _i64, _p, _i, _p, _i, _p, _p],
+    "q27h_last_error": [],
+    "q27h_abi_version": [],
+}
+_RESTYPE = {"q27h_kv_cache_bytes": _sz, "q27h_last_error": C.c_char_p}
+
+_lib = None
+
+
+def build_library(arch: str = "gfx950", jobs: int = 8) -> str:
+    """Compile csrc/*.hip for `arch` with hipcc into lib/libq27h.so (cross-compiles without a GPU)."""
+    subprocess.run(["make", "-s", "-C", os.path.join(_HERE, "csrc"), f"-j{jobs}", f"ARCH={arch}"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    """The loaded library with ctypes signatures set. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise Q27Error(-3, f"{LIB_PATH} is missing: build it with build_library() (or __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPE.get(name, C.c_int)
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        raise Q27Error(status, lib().q27h_last_error().decode())

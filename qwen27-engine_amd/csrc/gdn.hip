@@ -1,0 +1,284 @@
+// Gated-DeltaNet input stage: 4-tap causal conv + SiLU, L2 norm of the q/k heads, gates; fused for decode
+// (gdn_conv_l2, T <= 4 with state snapshots) and prefill (gdn_conv_prefill, M tokens, state plane flip), plus the
+// unfused twins gdn_conv / gdn_gates / l2norm_heads.
+//
+// Fused layout: 32 lanes (half a wave) per (head of 128 channels, chunk of tokens); lane p owns channels
+// 4p .. 4p+3, so every token row of a head is one 512-byte load and store, and the conv window of the last three
+// inputs stays in registers while the lanes walk the chunk's tokens. The L2 norm reproduces the reference's
+// warp-per-head order (src/ops.cu:318-330, 442-446): virtual lane v sums y[v]^2, y[v+32]^2, y[v+64]^2, y[v+96]^2
+// in that order, then the xor butterfly; those four values sit in lanes (p & 7) + 8k, fetched with ds_swizzle.
+#include "q27h_device.h"
+#include "q27h_internal.h"
+
+namespace q27h {
+namespace {
+
+__device__ __forceinline__ float conv4(float s0, float s1, float s2, float xn, const float (&w)[4]) {
+  float sum = 0.0f;  // src/ops.cu:419-423: sum = 0; sum += s0 w0; sum += s1 w1; sum += s2 w2; sum += x w3
+  sum += s0 * w[0];
+  sum += s1 * w[1];
+  sum += s2 * w[2];
+  sum += xn * w[3];
+  return sum;
+}
+
+// L2 norm of one 128-channel head held by a 32-lane half, lane p holding channels 4p + c.
+__device__ __forceinline__ void l2_head_lanes(float (&out)[4], float eps) {
+  float acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float sq = out[c] * out[c];
+    float a = 0.0f;
+    a += lane_pick<7, 0>(sq);
+    a += lane_pick<7, 8>(sq);
+    a += lane_pick<7, 16>(sq);
+    a += lane_pick<7, 24>(sq);
+    acc[c] = a;
+  }
+  const float tot = vwarp_sum4(acc);
+  const float scale = 1.0f / __builtin_sqrtf(tot / 128.0f + eps / 128.0f);
+  const float post = 1.0f / __builtin_sqrtf(128.0f);
+#pragma unroll
+  for (int c = 0; c < 4; c++) out[c] = (out[c] * scale) * post;
+}
+
+__device__ __forceinline__ void gate_one(const float* __restrict__ a, const float* __restrict__ b,
+                                         const float* __restrict__ ssm_a, const float* __restrict__ dt_bias,
+                                         float* __restrict__ g, float* __restrict__ beta, int t, int H, int hv) {
+  const size_t i = (size_t)t * H + hv;
+  beta[i] = q27_sigmoid(b[i]);
+  g[i] = q27_softplus(a[i] + dt_bias[hv]) * ssm_a[hv];
+}
+
+template <bool PREFILL>
+__global__ void __launch_bounds__(256) gdn_conv_fused_kernel(const float* __restrict__ x, const float* __restrict__ cw,
+                                                             float* __restrict__ planes, const int* __restrict__ in_plane,
+                                                             float* __restrict__ y, int C, int T, int snapshots,
+                                                             int n_norm_heads, float eps, const float* __restrict__ a,
+                                                             const float* __restrict__ b, const float* __restrict__ ssm_a,
+                                                             const float* __restrict__ dt_bias, float* __restrict__ g,
+                                                             float* __restrict__ beta, int H, int chunk, int nchunks) {
+  const int nheads = C / 128;
+  const int item = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (item >= nheads * nchunks) return;  // whole halves leave together
+  const int head = item / nchunks, ch = item % nchunks;
+  const int p = threadIdx.x & 31;
+  const int c0 = head * 128 + 4 * p;
+  const int t0 = ch * chunk, t1 = min(T, t0 + chunk);
+  const int pin = *in_plane;
+  float w[4][4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float4 wv = ld4(cw + 4 * (size_t)(c0 + c));
+    w[c][0] = wv.x; w[c][1] = wv.y; w[c][2] = wv.z; w[c][3] = wv.w;
+  }
+  // conv window: s0, s1, s2 = inputs t0-3, t0-2, t0-1 (state plane `pin` before the batch)
+  float s0[4], s1[4], s2[4];
+  {
+    const float* st = planes + ((size_t)pin * C + c0) * 3;  // 12 floats: channel c taps at 3c .. 3c+2
+    const float4 q0 = ld4(st), q1 = ld4(st + 4), q2 = ld4(st + 8);
+    const float sv[12] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) { s0[c] = sv[3 * c]; s1[c] = sv[3 * c + 1]; s2[c] = sv[3 * c + 2]; }
+    if (PREFILL && t0 > 0) {
+      const float4 r0 = ld4(x + (size_t)(t0 - 3) * C + c0), r1 = ld4(x + (size_t)(t0 - 2) * C + c0),
+                   r2 = ld4(x + (size_t)(t0 - 1) * C + c0);
+      s0[0] = r0.x; s0[1] = r0.y; s0[2] = r0.z; s0[3] = r0.w;
+      s1[0] = r1.x; s1[1] = r1.y; s1[2] = r1.z; s1[3] = r1.w;
+      s2[0] = r2.x; s2[1] = r2.y; s2[2] = r2.z; s2[3] = r2.w;
+    }
+  }
+  const bool norm = head < n_norm_heads;
+  for (int t = t0; t < t1; t++) {
+    const float4 xv = ld4(x + (size_t)t * C + c0);
+    const float xn[4] = {xv.x, xv.y, xv.z, xv.w};
+    float out[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      out[c] = q27_silu(conv4(s0[c], s1[c], s2[c], xn[c], w[c]));
+      s0[c] = s1[c]; s1[c] = s2[c]; s2[c] = xn[c];
+    }
+    if (!PREFILL && (snapshots || t == T - 1)) {
+      float* o = planes + ((size_t)t * C + c0) * 3;
+      st4(o, s0[0], s1[0], s2[0], s0[1]);
+      st4(o + 4, s1[1], s2[1], s0[2], s1[2]);
+      st4(o + 8, s2[2], s0[3], s1[3], s2[3]);
+    }
+    if (norm) l2_head_lanes(out, eps);
+    st4(y + (size_t)t * C + c0, out[0], out[1], out[2], out[3]);
+  }
+  if (!norm) {
+    const int hv = head - n_norm_heads;
+    for (int t = t0 + p; t < t1; t += 32) gate_one(a, b, ssm_a, dt_bias, g, beta, t, H, hv);
+  }
+  if (PREFILL && t1 == T) {  // state after the batch: inputs T-3 .. T-1 (from the old state when T < 3)
+    float* o = planes + ((size_t)(pin == 0 ? 1 : 0) * C + c0) * 3;
+    st4(o, s0[0], s1[0], s2[0], s0[1]);
+    st4(o + 4, s1[1], s2[1], s0[2], s1[2]);
+    st4(o + 8, s2[2], s0[3], s1[3], s2[3]);
+  }
+}
+
+// l2norm_heads for n = 128: 8 lanes per (token, head); lane q loads channels 4q + 32k (k = 0..3), i.e. the
+// virtual lanes 4q .. 4q+3 of the reference warp with their four values in summation order.
+__global__ void __launch_bounds__(256) l2norm128_kernel(float* __restrict__ x, int heads, int T, int stride, float eps) {
+  const int item = blockIdx.x * 32 + (threadIdx.x >> 3);
+  if (item >= heads * T) return;  // whole 8-lane groups leave together
+  const int t = item / heads, hd = item % heads;
+  const int q = threadIdx.x & 7;
+  float* p = x + (size_t)t * stride + (size_t)hd * 128 + 4 * q;
+  float v[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const float4 a = ld4(p + 32 * k);
+    v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+  }
+  float s[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) acc += v[k][c] * v[k][c];
+    s[c] = acc;
+  }
+  const float tot = vwarp_sum4(s);
+  const float scale = 1.0f / __builtin_sqrtf(tot / 128.0f + eps / 128.0f);
+  const float post = 1.0f / __builtin_sqrtf(128.0f);
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+    st4(p + 32 * k, (v[k][0] * scale) * post, (v[k][1] * scale) * post, (v[k][2] * scale) * post, (v[k][3] * scale) * post);
+}
+
+// l2norm_heads for any n (src/ops.cu:434-447 structure): 32 lanes per (token, head).
+__global__ void __launch_bounds__(256) l2norm_any_kernel(float* __restrict__ x, int n, int heads, int T, int stride, float eps) {
+  const int item = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (item >= heads * T) return;
+  const int t = item / heads, hd = item % heads, lane = threadIdx.x & 31;
+  float* p = x + (size_t)t * stride + (size_t)hd * n;
+  float acc = 0.0f;
+  for (int i = lane; i < n; i += 32) acc += p[i] * p[i];
+  acc = warp32_sum(acc);
+  const float scale = 1.0f / __builtin_sqrtf(acc / (float)n + eps / (float)n);
+  const float post = 1.0f / __builtin_sqrtf((float)n);
+  for (int i = lane; i < n; i += 32) p[i] = (p[i] * scale) * post;
+}
+
+__global__ void gdn_gates_kernel(const float* a, const float* b, const float* ssm_a, const float* dt_bias, float* g,
+                                 float* beta, int H, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  gate_one(a, b, ssm_a, dt_bias, g, beta, i / H, H, i % H);
+}
+
+// gdn_conv_kernel (src/ops.cu:407-431): one thread per channel, T tokens.
+__global__ void gdn_conv_kernel(const float* __restrict__ x, const float* __restrict__ cw, float* __restrict__ planes,
+                                const int* __restrict__ in_plane, float* __restrict__ y, int C, int T, int snapshots) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const float* st = planes + ((size_t)(*in_plane) * C + c) * 3;
+  float s0 = st[0], s1 = st[1], s2 = st[2];
+  const float w[4] = {cw[4 * c], cw[4 * c + 1], cw[4 * c + 2], cw[4 * c + 3]};
+  for (int t = 0; t < T; t++) {
+    const float xn = x[(size_t)t * C + c];
+    y[(size_t)t * C + c] = q27_silu(conv4(s0, s1, s2, xn, w));
+    s0 = s1; s1 = s2; s2 = xn;
+    if (snapshots || t == T - 1) {
+      float* o = planes + ((size_t)t * C + c) * 3;
+      o[0] = s0; o[1] = s1; o[2] = s2;
+    }
+  }
+}
+
+__global__ void flip_plane_kernel(int* p) { *p = *p == 0 ? 1 : 0; }
+__global__ void flip_plane_to_kernel(int* dst, const int* src) { *dst = *src == 0 ? 1 : 0; }
+
+int check_fused(const char* fn, const float* x, const float* w, const float* planes, const int* in_plane, const float* y,
+                int C, int T, int n_norm_heads, int H, const float* a, const float* b, const float* ssm_a,
+                const float* dt_bias, const float* g, const float* beta) {
+  if (C <= 0 || C % 128 || C / 128 - n_norm_heads != H || n_norm_heads < 0 || T < 0)
+    return fail(Q27H_ERR_SHAPE, std::string(fn) + ": bad shape");
+  if (!x || !w || !planes || !in_plane || !y) return fail(Q27H_ERR_ARG, std::string(fn) + ": null pointer");
+  if (H > 0 && (!a || !b || !ssm_a || !dt_bias || !g || !beta)) return fail(Q27H_ERR_ARG, std::string(fn) + ": null gate pointer");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(planes) || !aligned16(y))
+    return fail(Q27H_ERR_ARG, std::string(fn) + ": x, w, planes, y need 16-byte alignment");
+  return Q27H_OK;
+}
+
+}  // namespace
+}  // namespace q27h
+
+using namespace q27h;
+
+extern "C" int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,
+                                int snapshots, int n_norm_heads, float eps, const float* a, const float* b,
+                                const float* ssm_a, const float* dt_bias, float* g, float* beta, int H, q27h_stream_t s,
+                                const void* pf, size_t pf_bytes) {
+  (void)pf;
+  (void)pf_bytes;
+  if (int e = check_fused("gdn_conv_l2", x, w, planes, in_plane, y, C, T, n_norm_heads, H, a, b, ssm_a, dt_bias, g, beta))
+    return e;
+  if (T > 4) return fail(Q27H_ERR_SHAPE, "gdn_conv_l2: T must be <= 4 (4 state planes)");
+  if (T == 0) return Q27H_OK;
+  const int items = C / 128;
+  hipLaunchKernelGGL(gdn_conv_fused_kernel<false>, dim3((items + 7) / 8), dim3(256), 0, stream_of(s), x, w, planes, in_plane,
+                     y, C, T, snapshots, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, T, 1);
+  return check_launch("gdn_conv_l2");
+}
+
+extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C,
+                                     int M, int n_norm_heads, float eps, const float* a, const float* b, const float* ssm_a,
+                                     const float* dt_bias, float* g, float* beta, int H, q27h_stream_t s) {
+  if (int e = check_fused("gdn_conv_prefill", x, w, planes, in_plane, y, C, M, n_norm_heads, H, a, b, ssm_a, dt_bias, g, beta))
+    return e;
+  if (M == 0) return Q27H_OK;
+  const int chunk = 16;  // tokens per half-wave; >= 3 so a chunk's window never reaches past the previous chunk
+  const int nchunks = (M + chunk - 1) / chunk;
+  const long items = (long)(C / 128) * nchunks;
+  hipLaunchKernelGGL(gdn_conv_fused_kernel<true>, dim3((unsigned)((items + 7) / 8)), dim3(256), 0, stream_of(s), x, w, planes,
+                     in_plane, y, C, M, 0, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, chunk, nchunks);
+  return check_launch("gdn_conv_prefill");
+}
+
+extern "C" int q27h_l2norm_heads(float* x, int n, int heads, int T, int stride, float eps, q27h_stream_t s) {
+  if (n <= 0 || heads < 0 || T < 0) return fail(Q27H_ERR_SHAPE, "l2norm_heads: bad shape");
+  if (!x) return fail(Q27H_ERR_ARG, "l2norm_heads: null pointer");
+  const long items = (long)heads * T;
+  if (items == 0) return Q27H_OK;
+  if (n == 128 && stride % 4 == 0 && aligned16(x))
+    hipLaunchKernelGGL(l2norm128_kernel, dim3((unsigned)((items + 31) / 32)), dim3(256), 0, stream_of(s), x, heads, T, stride,
+                       eps);
+  else
+    hipLaunchKernelGGL(l2norm_any_kernel, dim3((unsigned)((items + 7) / 8)), dim3(256), 0, stream_of(s), x, n, heads, T, stride,
+                       eps);
+  return check_launch("l2norm_heads");
+}
+
+extern "C" int q27h_gdn_gates(const float* a, const float* b, const float* ssm_a, const float* dt_bias, float* g, float* beta,
+                              int H, int T, q27h_stream_t s) {
+  if (H <= 0 || T < 0) return fail(Q27H_ERR_SHAPE, "gdn_gates: bad shape");
+  if (T == 0) return Q27H_OK;
+  hipLaunchKernelGGL(gdn_gates_kernel, dim3((H * T + 127) / 128), dim3(128), 0, stream_of(s), a, b, ssm_a, dt_bias, g, beta, H,
+                     H * T);
+  return check_launch("gdn_gates");
+}
+
+extern "C" int q27h_gdn_conv(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,
+                             int snapshots, q27h_stream_t s) {
+  if (C <= 0 || T < 0 || T > 4) return fail(Q27H_ERR_SHAPE, "gdn_conv: bad shape (T <= 4)");
+  if (T == 0) return Q27H_OK;
+  hipLaunchKernelGGL(gdn_conv_kernel, dim3((C + 255) / 256), dim3(256), 0, stream_of(s), x, w, planes, in_plane, y, C, T,
+                     snapshots);
+  return check_launch("gdn_conv");
+}
+
+extern "C" int q27h_gdn_flip_plane(int* plane, q27h_stream_t s) {
+  if (!plane) return fail(Q27H_ERR_ARG, "gdn_flip_plane: null pointer");
+  hipLaunchKernelGGL(flip_plane_kernel, dim3(1), dim3(1), 0, stream_of(s), plane);
+  return check_launch("gdn_flip_plane");
+}
+
+extern "C" int q27h_flip_plane_to(int* dst, const int* src, q27h_stream_t s) {
+  if (!dst || !src) return fail(Q27H_ERR_ARG, "flip_plane_to: null pointer");
+  hipLaunchKernelGGL(flip_plane_to_kernel, dim3(1), dim3(1), 0, stream_of(s), dst, src);
+  return check_launch("flip_plane_to");
+}

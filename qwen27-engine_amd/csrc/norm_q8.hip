@@ -1,0 +1,306 @@
+// Row kernels that end in the q8_1 activation quantization: rmsnorm_q8, sum_norm_q8 / sum_norm_rows /
+// add_norm_rows (residual add + RMSNorm), quantize_q8_1, swiglu_q8, gated_rmsnorm_q8, and the unfused twins
+// rmsnorm / add / swiglu / gated_rmsnorm that the fused == unfused identity is checked against.
+//
+// Row engine (n = 5120): one 256-thread workgroup (4 waves) per row. Thread t loads five float4 at
+// t*4 + k*1024, k = 0..4, so it holds the values of the reference's 1024-thread layout (src/ops.cu:110-121:
+// thread u holds u + k*1024) for the four virtual threads u = 4t .. 4t+3. The per-virtual-thread partial sums
+// of squares, the 32-lane butterflies and the 32-way cross-warp butterfly are then formed from exactly the
+// same operands as the reference (q27h_device.h), while every global access is a 16-byte load or store and a
+// wave moves 1 KiB per instruction.
+#include "q27h_device.h"
+#include "q27h_internal.h"
+
+namespace q27h {
+namespace {
+
+// ---------------------------------------------------------------- row engine
+enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2 };
+
+template <int MODE>
+__global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x, const float* __restrict__ partial,
+                                                          const uint16_t* __restrict__ recv, const float* __restrict__ w,
+                                                          float eps, float* __restrict__ h, int8_t* __restrict__ xq,
+                                                          float* __restrict__ xd, float* __restrict__ xs) {
+  __shared__ float red[32];
+  const int t = threadIdx.x;
+  const size_t row = blockIdx.x;
+  const size_t base = row * kRowN + 4 * t;
+  float v[5][4];
+#pragma unroll
+  for (int k = 0; k < 5; k++) {
+    const float4 a = ld4(x + base + k * 1024);
+    v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+  }
+  if constexpr (MODE != kPlain) {
+#pragma unroll
+    for (int k = 0; k < 5; k++) {
+      const float4 p = ld4(partial + base + k * 1024);
+      const float pv[4] = {p.x, p.y, p.z, p.w};
+      if constexpr (MODE == kAddPartial) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[k][c] = v[k][c] + pv[c];
+      } else {
+        const uint2 rb = *(const uint2*)(recv + base + k * 1024);
+        const float rv[4] = {bf16_to_f((uint16_t)(rb.x & 0xffff)), bf16_to_f((uint16_t)(rb.x >> 16)),
+                             bf16_to_f((uint16_t)(rb.y & 0xffff)), bf16_to_f((uint16_t)(rb.y >> 16))};
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[k][c] = v[k][c] + (bf16_round(pv[c]) + rv[c]);
+      }
+      st4(x + base + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
+    }
+  }
+  // per virtual thread: t = 0; t += v[k]^2 for k = 0..4 (src/ops.cu:96-98)
+  float s[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 5; k++) acc += v[k][c] * v[k][c];
+    s[c] = acc;
+  }
+  const float wsum = vwarp_sum4(s);
+  if ((t & 7) == 0) red[t >> 3] = wsum;
+  __syncthreads();
+  const float tot = warp32_sum(red[t & 31]);
+  const float scale = 1.0f / __builtin_sqrtf(tot / (float)kRowN + eps);
+#pragma unroll
+  for (int k = 0; k < 5; k++) {
+    const float4 wv = ld4(w + 4 * t + k * 1024);
+    const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    float y[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) y[c] = scale * v[k][c] * ww[c];
+    if (h) st4(h + base + k * 1024, y[0], y[1], y[2], y[3]);
+    q8_1_store4(y, xq, xd, xs, base + k * 1024);
+  }
+}
+
+// ---------------------------------------------------------------- flat q8_1 producers
+// Thread i handles values 4i .. 4i+3 of a flat array (n % 32 == 0, so a q8 block is 8 aligned lanes).
+template <bool SWIGLU>
+__global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                      int8_t* __restrict__ xq, float* __restrict__ xd,
+                                                      float* __restrict__ xs, size_t n) {
+  const size_t i0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i0 >= n) return;  // whole 8-lane groups leave together
+  const float4 a = ld4(g + i0);
+  float y[4] = {a.x, a.y, a.z, a.w};
+  if constexpr (SWIGLU) {
+    const float4 b = ld4(u + i0);
+    const float ub[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) y[c] = q27_silu(y[c]) * ub[c];
+  }
+  q8_1_store4(y, xq, xd, xs, i0);
+}
+
+// ---------------------------------------------------------------- gated RMSNorm -> q8_1 (heads of 128)
+// 32 lanes per head, lane p holds values 4p .. 4p+3; a 256-thread workgroup covers 8 heads. The reference's
+// 128-thread block_sum (4 warps) becomes: per virtual warp (8 lanes) vwarp_sum4, then the second stage over 4
+// warp sums with zeros in lanes 4..31, i.e. (w0 + w2) + (w1 + w3) = lane xor 16, then lane xor 8.
+__global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __restrict__ o, const float* __restrict__ w,
+                                                               const float* __restrict__ z, int8_t* __restrict__ xq,
+                                                               float* __restrict__ xd, float eps, float* __restrict__ xs,
+                                                               int heads) {
+  const int head = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (head >= heads) return;  // whole 32-lane halves leave together
+  const int p = threadIdx.x & 31;
+  const size_t i0 = (size_t)head * 128 + 4 * p;
+  const float4 ov = ld4(o + i0);
+  const float v[4] = {ov.x, ov.y, ov.z, ov.w};
+  float s[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) s[c] = v[c] * v[c];
+  float tsum = vwarp_sum4(s);
+  tsum = tsum + 0.0f;  // the reference adds the zero lanes 4..31 (xor 16, 8, 4 steps); x + 0 == x for x >= +0
+  tsum += lane_xor<16>(tsum);
+  tsum += lane_xor<8>(tsum);
+  const float scale = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
+  const float4 wv = ld4(w + 4 * p);
+  const float4 zv = ld4(z + i0);
+  const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  const float zz[4] = {zv.x, zv.y, zv.z, zv.w};
+  float y[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * q27_silu(zz[c]);
+  q8_1_store4(y, xq, xd, xs, i0);
+}
+
+// ---------------------------------------------------------------- unfused twins (reference structure)
+// rmsnorm_kernel (src/ops.cu:57-68): block of B threads per row, thread t sums x[i]^2 for i = t, t + B, ...
+__global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                       float* __restrict__ y, int n, float eps, int ystride) {
+  __shared__ float red[32];
+  const float* xr = x + (size_t)blockIdx.x * n;
+  float* yr = y + (size_t)blockIdx.x * ystride;
+  float t = 0.0f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = xr[i];
+    t += v * v;
+  }
+  t = block_sum_ref(t, red, blockDim.x);
+  const float scale = 1.0f / __builtin_sqrtf(t / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = scale * xr[i] * w[i];
+}
+
+__global__ void add_kernel(const float* __restrict__ x, const float* __restrict__ a, float* __restrict__ y, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = x[i] + a[i];
+}
+
+__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = q27_silu(g[i]) * u[i];
+}
+
+__global__ void set_int_kernel(int* p, int v) { *p = v; }
+
+// gated_rmsnorm_kernel (src/ops.cu:574-585): 128 threads per head of n values.
+__global__ void __launch_bounds__(128) gated_rmsnorm_kernel(const float* __restrict__ o, const float* __restrict__ w,
+                                                            const float* __restrict__ z, float* __restrict__ y, int n,
+                                                            float eps) {
+  __shared__ float red[32];
+  const size_t off = (size_t)blockIdx.x * n;
+  float t = 0.0f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = o[off + i];
+    t += v * v;
+  }
+  t = block_sum_ref(t, red, blockDim.x);
+  const float scale = 1.0f / __builtin_sqrtf(t / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) y[off + i] = (scale * o[off + i] * w[i]) * q27_silu(z[off + i]);
+}
+
+int check_row_args(const char* fn, int n, int rows, const float* x, const float* w, const float* h, const int8_t* xq,
+                   const float* xd) {
+  if (n != kRowN) return fail(Q27H_ERR_SHAPE, std::string(fn) + ": n must be 5120");
+  if (rows < 0) return fail(Q27H_ERR_SHAPE, std::string(fn) + ": rows < 0");
+  if (!x || !w || !xq || !xd) return fail(Q27H_ERR_ARG, std::string(fn) + ": null pointer");
+  if (!aligned16(x) || !aligned16(w) || (h && !aligned16(h)) || !aligned4(xq))
+    return fail(Q27H_ERR_ARG, std::string(fn) + ": x, w, h need 16-byte and xq 4-byte alignment");
+  return Q27H_OK;
+}
+
+template <int MODE>
+int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* recv, const float* w, float eps, float* h,
+                int8_t* xq, float* xd, float* xs, int rows, q27h_stream_t s) {
+  if (rows == 0) return Q27H_OK;
+  hipLaunchKernelGGL(row_norm_q8_kernel<MODE>, dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h, xq, xd,
+                     xs);
+  return check_launch(fn);
+}
+
+int launch_flat(const char* fn, bool swiglu, const float* g, const float* u, int8_t* xq, float* xd, float* xs, size_t n,
+                q27h_stream_t s) {
+  if (n == 0) return Q27H_OK;
+  if (!g || !xq || !xd || (swiglu && !u)) return fail(Q27H_ERR_ARG, std::string(fn) + ": null pointer");
+  if (!aligned16(g) || (swiglu && !aligned16(u)) || !aligned4(xq))
+    return fail(Q27H_ERR_ARG, std::string(fn) + ": inputs need 16-byte and xq 4-byte alignment");
+  const size_t blocks = (n / 4 + 255) / 256;
+  if (swiglu)
+    hipLaunchKernelGGL(flat_q8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
+  else
+    hipLaunchKernelGGL(flat_q8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
+  return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace q27h
+
+using namespace q27h;
+
+extern "C" int q27h_rmsnorm_q8(const float* x, const float* w, float* h, int8_t* xq, float* xd, int n, int rows, float eps,
+                               q27h_stream_t s, float* xs) {
+  if (int e = check_row_args("rmsnorm_q8", n, rows, x, w, h, xq, xd)) return e;
+  return launch_rows<kPlain>("rmsnorm_q8", const_cast<float*>(x), nullptr, nullptr, w, eps, h, xq, xd, xs, rows, s);
+}
+
+extern "C" int q27h_sum_norm_q8(float* x, const float* partial, int n, int rows, const void* ar, const float* w, float eps,
+                                float* h, int8_t* xq, float* xd, q27h_stream_t s, const void* pf, size_t pf_bytes) {
+  (void)pf;
+  (void)pf_bytes;
+  if (ar) return fail(Q27H_ERR_UNSUPPORTED, "sum_norm_q8: the cross-card exchange (ar != null) is not part of this build");
+  if (int e = check_row_args("sum_norm_q8", n, rows, x, w, h, xq, xd)) return e;
+  if (!partial || !aligned16(partial)) return fail(Q27H_ERR_ARG, "sum_norm_q8: partial null or misaligned");
+  return launch_rows<kAddPartial>("sum_norm_q8", x, partial, nullptr, w, eps, h, xq, xd, nullptr, rows, s);
+}
+
+extern "C" int q27h_sum_norm_rows(float* x, const float* partial, int n, int M, const void* ex, const float* w, float eps,
+                                  float* h, int8_t* xq, float* xd, float* xs, q27h_stream_t s) {
+  if (ex) return fail(Q27H_ERR_UNSUPPORTED, "sum_norm_rows: the cross-card exchange (ex != null) is not part of this build");
+  if (int e = check_row_args("sum_norm_rows", n, M, x, w, h, xq, xd)) return e;
+  if (!partial || !aligned16(partial)) return fail(Q27H_ERR_ARG, "sum_norm_rows: partial null or misaligned");
+  return launch_rows<kAddPartial>("sum_norm_rows", x, partial, nullptr, w, eps, h, xq, xd, xs, M, s);
+}
+
+extern "C" int q27h_add_norm_rows(float* x, const float* partial, const uint16_t* recv, int n, int M, const float* w,
+                                  float eps, float* h, int8_t* xq, float* xd, float* xs, q27h_stream_t s) {
+  if (int e = check_row_args("add_norm_rows", n, M, x, w, h, xq, xd)) return e;
+  if (!partial || !aligned16(partial)) return fail(Q27H_ERR_ARG, "add_norm_rows: partial null or misaligned");
+  if (recv) {
+    if (((uintptr_t)recv & 7u) != 0) return fail(Q27H_ERR_ARG, "add_norm_rows: recv needs 8-byte alignment");
+    return launch_rows<kAddBf16Recv>("add_norm_rows", x, partial, recv, w, eps, h, xq, xd, xs, M, s);
+  }
+  return launch_rows<kAddPartial>("add_norm_rows", x, partial, nullptr, w, eps, h, xq, xd, xs, M, s);
+}
+
+extern "C" int q27h_quantize_q8_1(const float* x, int8_t* xq, float* xd, int K, int ncols, q27h_stream_t s, float* xs) {
+  if (K <= 0 || K % 32 || ncols < 0) return fail(Q27H_ERR_SHAPE, "quantize_q8_1: K must be a positive multiple of 32");
+  return launch_flat("quantize_q8_1", false, x, nullptr, xq, xd, xs, (size_t)K * (size_t)ncols, s);
+}
+
+extern "C" int q27h_swiglu_q8(const float* g, const float* u, int8_t* xq, float* xd, int n, q27h_stream_t s, float* xs) {
+  if (n < 0 || n % 32) return fail(Q27H_ERR_SHAPE, "swiglu_q8: n % 32");
+  return launch_flat("swiglu_q8", true, g, u, xq, xd, xs, (size_t)n, s);
+}
+
+extern "C" int q27h_gated_rmsnorm_q8(const float* o, const float* w, const float* z, int8_t* xq, float* xd, int heads,
+                                     float eps, q27h_stream_t s, float* xs) {
+  if (heads < 0) return fail(Q27H_ERR_SHAPE, "gated_rmsnorm_q8: heads < 0");
+  if (heads == 0) return Q27H_OK;
+  if (!o || !w || !z || !xq || !xd) return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: null pointer");
+  if (!aligned16(o) || !aligned16(w) || !aligned16(z) || !aligned4(xq))
+    return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: o, w, z need 16-byte and xq 4-byte alignment");
+  hipLaunchKernelGGL(gated_rmsnorm_q8_kernel, dim3((heads + 7) / 8), dim3(256), 0, stream_of(s), o, w, z, xq, xd, eps, xs,
+                     heads);
+  return check_launch("gated_rmsnorm_q8");
+}
+
+extern "C" int q27h_rmsnorm(const float* x, const float* w, float* y, int n, int rows, float eps, q27h_stream_t s,
+                            int ystride) {
+  if (n <= 0 || rows < 0) return fail(Q27H_ERR_SHAPE, "rmsnorm: bad shape");
+  if (rows == 0) return Q27H_OK;
+  if (!x || !w || !y) return fail(Q27H_ERR_ARG, "rmsnorm: null pointer");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(n >= 1024 ? 1024 : 256), 0, stream_of(s), x, w, y, n, eps,
+                     ystride ? ystride : n);
+  return check_launch("rmsnorm");
+}
+
+extern "C" int q27h_add(const float* x, const float* a, float* y, int n, q27h_stream_t s) {
+  if (n < 0) return fail(Q27H_ERR_SHAPE, "add: n < 0");
+  if (n == 0) return Q27H_OK;
+  hipLaunchKernelGGL(add_kernel, dim3((n + 255) / 256), dim3(256), 0, stream_of(s), x, a, y, n);
+  return check_launch("add");
+}
+
+extern "C" int q27h_swiglu(const float* g, const float* u, float* y, int n, q27h_stream_t s) {
+  if (n < 0) return fail(Q27H_ERR_SHAPE, "swiglu: n < 0");
+  if (n == 0) return Q27H_OK;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, stream_of(s), g, u, y, n);
+  return check_launch("swiglu");
+}
+
+extern "C" int q27h_set_int(int* p, int v, q27h_stream_t s) {
+  if (!p) return fail(Q27H_ERR_ARG, "set_int: null pointer");
+  hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, stream_of(s), p, v);
+  return check_launch("set_int");
+}
+
+extern "C" int q27h_gated_rmsnorm(const float* o, const float* w, const float* z, float* y, int n, int heads, float eps,
+                                  q27h_stream_t s) {
+  if (n <= 0 || heads < 0) return fail(Q27H_ERR_SHAPE, "gated_rmsnorm: bad shape");
+  if (heads == 0) return Q27H_OK;
+  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(heads), dim3(128), 0, stream_of(s), o, w, z, y, n, eps);
+  return check_launch("gated_rmsnorm");
+}

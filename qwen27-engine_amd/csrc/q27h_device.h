@@ -1,0 +1,234 @@
+// Device helpers shared by the gfx950 kernels of the fused per-layer ops.
+//
+// Numerics contract (identical on the CPU checker): no FP contraction (built with -ffp-contract=off),
+// rsqrt = 1.0f / sqrtf, correctly rounded division and sqrt, exp/log/sin/cos from the routines below.
+// Lane exchanges use DPP (quad permutes, 16-lane row rotate) and ds_swizzle (xor inside 32 lanes); they
+// only move values, so every reduction below adds exactly the operands the reference's 32-lane
+// butterflies add (src/ops.cu:34-50, src/common.cuh:68-87).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q27h {
+
+constexpr int kRowN = 5120;  // hidden size of the row kernels (n must be 5120, src/ops.cu:699)
+
+// ---------------------------------------------------------------- lane exchange
+// Value of lane (lane ^ M), M in {1, 2, 4, 8, 16, 24}: stays inside an aligned group of 32 lanes.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (M == 1) r = __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false);        // quad_perm [1,0,3,2]
+  else if constexpr (M == 2) r = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  else if constexpr (M == 8) r = __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false);  // row_ror:8 (16-lane rows)
+  else r = __builtin_amdgcn_ds_swizzle(iv, (M << 10) | 0x1F);                          // bit mode: lane ^ M
+  return __builtin_bit_cast(float, r);
+}
+// Value of lane ((lane & AND) | OR) inside the same 32-lane group (ds_swizzle bit mode).
+template <int AND, int OR>
+__device__ __forceinline__ float lane_pick(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, (OR << 5) | AND));
+}
+// Value of lane (lane ^ 32): crosses the two halves of the wave (ds_bpermute).
+__device__ __forceinline__ float lane_xor32(float v) {
+  const int lane = __lane_id();
+  const int iv = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, iv));
+}
+
+// The reference's warp_sum (xor 16, 8, 4, 2, 1 over the 32 lanes of a lane group).
+__device__ __forceinline__ float warp32_sum(float v) {
+  v += lane_xor<16>(v);
+  v += lane_xor<8>(v);
+  v += lane_xor<4>(v);
+  v += lane_xor<2>(v);
+  v += lane_xor<1>(v);
+  return v;
+}
+
+// Reference block_sum (src/ops.cu:40-50) for a block of `nthreads` threads (multiple of 32), one value per
+// thread, thread t = threadIdx.x. `red` is 32 floats of LDS. All threads must call it.
+__device__ __forceinline__ float block_sum_ref(float v, float* red, int nthreads) {
+  const int t = threadIdx.x;
+  v = warp32_sum(v);
+  __syncthreads();
+  if ((t & 31) == 0) red[t >> 5] = v;
+  __syncthreads();
+  v = (t & 31) < (nthreads >> 5) ? red[t & 31] : 0.0f;
+  return warp32_sum(v);
+}
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32: round to nearest even, subnormals kept
+}
+__device__ __forceinline__ float h2f_bits(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ float fp16_round(float f) { return (float)(_Float16)f; }
+// __float2bfloat16 (round to nearest even; NaN stays a quiet NaN)
+__device__ __forceinline__ float bf16_round(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return __builtin_bit_cast(float, (u | 0x00400000u) & 0xffff0000u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __builtin_bit_cast(float, u & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+// ---------------------------------------------------------------- transcendental functions
+// exp: Cody-Waite reduction x = k ln2 + r, degree-7 Taylor polynomial of e^r (Horner, fma), ldexp.
+// Same operations and constants as the CPU checker (Muller, Elementary Functions, ch. 11).
+__device__ __forceinline__ float q27_expf(float x) {
+  if (x != x) return x + x;
+  if (x > 88.7228394f) return __builtin_huge_valf();
+  if (x < -103.972084f) return 0.0f;
+  const float k = __builtin_rintf(x * 1.44269502f);
+  float r = __builtin_fmaf(-k, 0.693145752f, x);
+  r = __builtin_fmaf(-k, 1.42860677e-06f, r);
+  float p = 1.98412698e-4f;
+  p = __builtin_fmaf(p, r, 1.38888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)k);
+}
+
+// log for the softplus gate: x = 2^e m, m in [sqrt(1/2), sqrt(2)), s = f / (2 + f), log m = 2 atanh(s) as an
+// odd series to s^11, log x = e ln2_hi + (e ln2_lo + log m).
+__device__ __forceinline__ float q27_logf(float x) {
+  if (x != x || x < 0.0f) return __builtin_nanf("");
+  if (x == 0.0f) return -__builtin_huge_valf();
+  if (x == __builtin_huge_valf()) return x;
+  int e = 0;
+  if (x < 1.17549435e-38f) { x *= 8388608.0f; e = -23; }
+  uint32_t ix = __builtin_bit_cast(uint32_t, x);
+  e += (int)((ix >> 23) & 0xff) - 127;
+  ix = (ix & 0x007fffffu) | 0x3f800000u;
+  float m = __builtin_bit_cast(float, ix);
+  if (m > 1.41421354f) { m *= 0.5f; e += 1; }
+  const float f = m - 1.0f;
+  const float s = f / (2.0f + f);
+  const float z = s * s;
+  float R = 1.81818187e-1f;
+  R = __builtin_fmaf(R, z, 2.22222224e-1f);
+  R = __builtin_fmaf(R, z, 2.85714298e-1f);
+  R = __builtin_fmaf(R, z, 4.00000006e-1f);
+  R = __builtin_fmaf(R, z, 6.66666687e-1f);
+  R = R * z;
+  const float logm = __builtin_fmaf(s, R, s + s);
+  const float fe = (float)e;
+  return __builtin_fmaf(fe, 0.693145752f, __builtin_fmaf(fe, 1.42860677e-06f, logm));
+}
+
+__device__ __forceinline__ float q27_silu(float x) { return x / (1.0f + q27_expf(-x)); }
+__device__ __forceinline__ float q27_sigmoid(float x) { return 1.0f / (1.0f + q27_expf(-x)); }
+__device__ __forceinline__ float q27_softplus(float x) { return x > 20.0f ? x : q27_logf(1.0f + q27_expf(x)); }
+
+// sin and cos of a float angle: Cody-Waite reduction by pi/2 in double (pio2 split 33 + 53 bits), Taylor
+// polynomials to degree 21 / 20 on |r| <= pi/4, separate double multiplies and adds, one rounding to float.
+__device__ __forceinline__ void q27_sincos(float theta, float* s_out, float* c_out) {
+  const double th = (double)theta;
+  const double kd = __builtin_rint(th * 6.36619772367581382433e-01);
+  const double r = (th - kd * 1.57079632673412561417e+00) - kd * 6.07710050650619224932e-11;
+  const double z = r * r;
+  double sp = 1.9572941063391263e-20;
+  sp = sp * z + -8.22063524662433e-18;
+  sp = sp * z + 2.8114572543455206e-15;
+  sp = sp * z + -7.647163731819816e-13;
+  sp = sp * z + 1.6059043836821613e-10;
+  sp = sp * z + -2.505210838544172e-08;
+  sp = sp * z + 2.7557319223985893e-06;
+  sp = sp * z + -0.0001984126984126984;
+  sp = sp * z + 0.008333333333333333;
+  sp = sp * z + -0.16666666666666666;
+  const double sn = r + (r * z) * sp;
+  double cp = 4.110317623312165e-19;
+  cp = cp * z + -1.5619206968586225e-16;
+  cp = cp * z + 4.779477332387385e-14;
+  cp = cp * z + -1.1470745597729725e-11;
+  cp = cp * z + 2.08767569878681e-09;
+  cp = cp * z + -2.755731922398589e-07;
+  cp = cp * z + 2.48015873015873e-05;
+  cp = cp * z + -0.001388888888888889;
+  cp = cp * z + 0.041666666666666664;
+  cp = cp * z + -0.5;
+  const double cs = 1.0 + z * cp;
+  const int q = (int)(long long)kd & 3;
+  double s, c;
+  if (q == 0) { s = sn; c = cs; }
+  else if (q == 1) { s = cs; c = -sn; }
+  else if (q == 2) { s = -sn; c = -cs; }
+  else { s = -cs; c = sn; }
+  *s_out = (float)s;
+  *c_out = (float)c;
+}
+
+// ---------------------------------------------------------------- q8 rounding
+// roundf(y / d) for |y| <= 127 d, d > 0 (the q8_1 rule of src/common.cuh:76). y * (1/d) is within 2.3e-5 of the
+// correctly rounded quotient, so away from the half-integers it rounds the same way and rintf == roundf; within
+// 2^-12 of a half-integer (or for non-finite 1/d) the IEEE quotient is taken.
+__device__ __forceinline__ int q8_round_div(float y, float d, float rd) {
+  const float a = y * rd;
+  const float fa = __builtin_fabsf(a);
+  const float fr = fa - __builtin_floorf(fa);
+  if (__builtin_fabsf(fr - 0.5f) > 2.44140625e-4f) return (int)__builtin_rintf(a);
+  return (int)__builtin_roundf(y / d);
+}
+
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
+}
+
+// q8_1 of 32 consecutive values held by 8 consecutive lanes, 4 values per lane (the lane's values are flat
+// indices i0 .. i0 + 3, i0 % 4 == 0, lanes (i0 / 4) % 8 = 0..7 of an aligned 8-lane group):
+// amax over the block, d = amax / 127, q = roundf(y / d) (0 when amax == 0), xd = fp16(d) as f32 and the
+// optional per-16 sums of the unquantized values in the reference's butterfly order (xor 8, 4, 2, 1 over the
+// 16 virtual lanes = lane xor 2, lane xor 1, then value pairs (0,2)(1,3), then (0,1)).
+__device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restrict__ xq, float* __restrict__ xd,
+                                            float* __restrict__ xs, size_t i0) {
+  float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(y[0]), __builtin_fabsf(y[1])),
+                               __builtin_fmaxf(__builtin_fabsf(y[2]), __builtin_fabsf(y[3])));
+  amax = __builtin_fmaxf(amax, lane_xor<4>(amax));
+  amax = __builtin_fmaxf(amax, lane_xor<2>(amax));
+  amax = __builtin_fmaxf(amax, lane_xor<1>(amax));
+  const float d = amax / 127.0f;
+  int q[4] = {0, 0, 0, 0};
+  if (amax != 0.0f) {
+    const float rd = 1.0f / d;
+#pragma unroll
+    for (int c = 0; c < 4; c++) q[c] = q8_round_div(y[c], d, rd);
+  }
+  *(uint32_t*)(xq + i0) = pack4_i8(q[0], q[1], q[2], q[3]);
+  const int sub = (int)((i0 >> 2) & 7);
+  if (sub == 0) xd[i0 >> 5] = fp16_round(d);
+  if (xs) {
+    float u[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) u[c] = y[c] + lane_xor<2>(y[c]);
+#pragma unroll
+    for (int c = 0; c < 4; c++) u[c] = u[c] + lane_xor<1>(u[c]);
+    const float tot = (u[0] + u[2]) + (u[1] + u[3]);
+    if ((sub & 3) == 0) xs[i0 >> 4] = tot;
+  }
+}
+
+// First stage of the reference block_sum for 32-thread virtual warps whose thread t holds the values of
+// virtual lanes 4 (t & 7) + c, c = 0..3 (8 physical lanes = one virtual warp): xor 16, 8, 4 of the virtual
+// lanes are lane xor 4, 2, 1; xor 2 and 1 pair the lane's own values. Returns the virtual warp's sum.
+__device__ __forceinline__ float vwarp_sum4(float (&s)[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; c++) s[c] += lane_xor<4>(s[c]);
+#pragma unroll
+  for (int c = 0; c < 4; c++) s[c] += lane_xor<2>(s[c]);
+#pragma unroll
+  for (int c = 0; c < 4; c++) s[c] += lane_xor<1>(s[c]);
+  return (s[0] + s[2]) + (s[1] + s[3]);
+}
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*)p; }
+__device__ __forceinline__ void st4(float* p, float a, float b, float c, float d) { *(float4*)p = make_float4(a, b, c, d); }
+
+}  // namespace q27h

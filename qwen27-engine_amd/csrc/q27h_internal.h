@@ -1,0 +1,20 @@
+// Host-side plumbing shared by the launchers: status codes, the per-thread error text, launch checks.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/q27h.h"
+
+namespace q27h {
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+// Checks the launch that was just enqueued; returns Q27H_OK or Q27H_ERR_HIP with the HIP error text.
+int check_launch(const char* what);
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
+inline hipStream_t stream_of(q27h_stream_t s) { return (hipStream_t)s; }
+
+}  // namespace q27h

@@ -1,0 +1,138 @@
+"""The reference engine's launchers (src/ops.h, src/prefill.h, src/qmat.h) over torch device tensors.
+
+Same names, argument order and defaults as the C++ declarations; tensors stand for device pointers (None for
+nullptr), `s` is a HIP stream handle (int) and defaults to torch's current stream. Every function only
+enqueues work. A bad shape or a failed launch raises Q27Error (the reference throws std::runtime_error).
+"""
+from __future__ import annotations
+
+from ._lib import check, lib
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(s):
+    if s is not None:
+        return s
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---------------------------------------------------------------- ops.h
+def rmsnorm(x, w, y, n, rows, eps, s=None, ystride=0):
+    check(lib().q27h_rmsnorm(_ptr(x), _ptr(w), _ptr(y), n, rows, eps, _stream(s), ystride))
+
+
+def add(x, a, y, n, s=None):
+    check(lib().q27h_add(_ptr(x), _ptr(a), _ptr(y), n, _stream(s)))
+
+
+def swiglu(g, u, y, n, s=None):
+    check(lib().q27h_swiglu(_ptr(g), _ptr(u), _ptr(y), n, _stream(s)))
+
+
+def set_int(p, v, s=None):
+    check(lib().q27h_set_int(_ptr(p), v, _stream(s)))
+
+
+def get_rows_iq2_s(table, row_bytes, ids, T, y, n, s=None, img=None):
+    check(lib().q27h_get_rows_iq2_s(_ptr(table), row_bytes, _ptr(ids), T, _ptr(y), n, _stream(s), _ptr(img)))
+
+
+def get_rows_q4_k(table, row_bytes, ids, T, y, n, s=None, img=None):
+    check(lib().q27h_get_rows_q4_k(_ptr(table), row_bytes, _ptr(ids), T, _ptr(y), n, _stream(s), _ptr(img)))
+
+
+def get_rows_q6_k(table, row_bytes, ids, T, y, n, s=None, img=None):
+    check(lib().q27h_get_rows_q6_k(_ptr(table), row_bytes, _ptr(ids), T, _ptr(y), n, _stream(s), _ptr(img)))
+
+
+def get_rows_q8_0(table, row_bytes, ids, T, y, n, s=None, img=None):
+    check(lib().q27h_get_rows_q8_0(_ptr(table), row_bytes, _ptr(ids), T, _ptr(y), n, _stream(s), _ptr(img)))
+
+
+def gdn_gates(a, b, ssm_a, dt_bias, g, beta, H, T, s=None):
+    check(lib().q27h_gdn_gates(_ptr(a), _ptr(b), _ptr(ssm_a), _ptr(dt_bias), _ptr(g), _ptr(beta), H, T, _stream(s)))
+
+
+def gdn_conv(x, w, planes, in_plane, y, C, T, snapshots, s=None):
+    check(lib().q27h_gdn_conv(_ptr(x), _ptr(w), _ptr(planes), _ptr(in_plane), _ptr(y), C, T, int(snapshots), _stream(s)))
+
+
+def l2norm_heads(x, n, heads, T, stride, eps, s=None):
+    check(lib().q27h_l2norm_heads(_ptr(x), n, heads, T, stride, eps, _stream(s)))
+
+
+def gated_rmsnorm(o, w, z, y, n, heads, eps, s=None):
+    check(lib().q27h_gated_rmsnorm(_ptr(o), _ptr(w), _ptr(z), _ptr(y), n, heads, eps, _stream(s)))
+
+
+def kv_cache_bytes(nkvh, n_ctx, q8):
+    return lib().q27h_kv_cache_bytes(nkvh, n_ctx, int(q8))
+
+
+def attn_prep(qg, k, v, q_norm, k_norm, qn, kcache, vcache, pos0, T, eps, theta_scale, nqh, nkvh, n_ctx, q8, s=None,
+              pf=None, pf_bytes=0, rope3=None, rdelta=None):
+    check(lib().q27h_attn_prep(_ptr(qg), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), _ptr(qn), _ptr(kcache),
+                               _ptr(vcache), _ptr(pos0), T, eps, theta_scale, nqh, nkvh, n_ctx, int(q8), _stream(s),
+                               _ptr(pf), pf_bytes, _ptr(rope3), _ptr(rdelta)))
+
+
+def rmsnorm_q8(x, w, h, xq, xd, n, rows, eps, s=None, xs=None):
+    check(lib().q27h_rmsnorm_q8(_ptr(x), _ptr(w), _ptr(h), _ptr(xq), _ptr(xd), n, rows, eps, _stream(s), _ptr(xs)))
+
+
+def sum_norm_q8(x, partial, n, rows, ar, w, eps, h, xq, xd, s=None, pf=None, pf_bytes=0):
+    check(lib().q27h_sum_norm_q8(_ptr(x), _ptr(partial), n, rows, _ptr(ar), _ptr(w), eps, _ptr(h), _ptr(xq), _ptr(xd),
+                                 _stream(s), _ptr(pf), pf_bytes))
+
+
+def swiglu_q8(g, u, xq, xd, n, s=None, xs=None):
+    check(lib().q27h_swiglu_q8(_ptr(g), _ptr(u), _ptr(xq), _ptr(xd), n, _stream(s), _ptr(xs)))
+
+
+def gated_rmsnorm_q8(o, w, z, xq, xd, heads, eps, s=None, xs=None):
+    check(lib().q27h_gated_rmsnorm_q8(_ptr(o), _ptr(w), _ptr(z), _ptr(xq), _ptr(xd), heads, eps, _stream(s), _ptr(xs)))
+
+
+def gdn_conv_l2(x, w, planes, in_plane, y, C, T, snapshots, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, s=None,
+                pf=None, pf_bytes=0):
+    check(lib().q27h_gdn_conv_l2(_ptr(x), _ptr(w), _ptr(planes), _ptr(in_plane), _ptr(y), C, T, int(snapshots),
+                                 n_norm_heads, eps, _ptr(a), _ptr(b), _ptr(ssm_a), _ptr(dt_bias), _ptr(g), _ptr(beta), H,
+                                 _stream(s), _ptr(pf), pf_bytes))
+
+
+# ---------------------------------------------------------------- prefill.h
+def gdn_conv_prefill(x, w, planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, s=None):
+    check(lib().q27h_gdn_conv_prefill(_ptr(x), _ptr(w), _ptr(planes), _ptr(in_plane), _ptr(y), C, M, n_norm_heads, eps,
+                                      _ptr(a), _ptr(b), _ptr(ssm_a), _ptr(dt_bias), _ptr(g), _ptr(beta), H, _stream(s)))
+
+
+def gdn_flip_plane(plane, s=None):
+    check(lib().q27h_gdn_flip_plane(_ptr(plane), _stream(s)))
+
+
+def flip_plane_to(dst, src, s=None):
+    check(lib().q27h_flip_plane_to(_ptr(dst), _ptr(src), _stream(s)))
+
+
+def sum_norm_rows(x, partial, n, M, ex, w, eps, h, xq, xd, xs, s=None):
+    check(lib().q27h_sum_norm_rows(_ptr(x), _ptr(partial), n, M, _ptr(ex), _ptr(w), eps, _ptr(h), _ptr(xq), _ptr(xd),
+                                   _ptr(xs), _stream(s)))
+
+
+def add_norm_rows(x, partial, recv, n, M, w, eps, h, xq, xd, xs, s=None):
+    check(lib().q27h_add_norm_rows(_ptr(x), _ptr(partial), _ptr(recv), n, M, _ptr(w), eps, _ptr(h), _ptr(xq), _ptr(xd),
+                                   _ptr(xs), _stream(s)))
+
+
+# ---------------------------------------------------------------- qmat.h
+def quantize_q8_1(x, xq, xd, K, ncols, s=None, xs=None):
+    check(lib().q27h_quantize_q8_1(_ptr(x), _ptr(xq), _ptr(xd), K, ncols, _stream(s), _ptr(xs)))

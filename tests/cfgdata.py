@@ -1,0 +1,89 @@
+"""Seeded synthetic inputs for the five BASELINE.json configurations (numpy, host side).
+
+cfg1  RMSNorm -> q8_1 on one 5120 row, N(0,1) with 0.1% of the values x50, w ~ N(1, 0.1), eps 1e-6
+cfg2  decode verify pass, T = 4: rows [4][5120]; gate/up [4][17408] ~ N(0, 2) (standard deviation 2);
+      q|gate [4][24][512], k, v [4][4][256]; positions 150000..150003; q8_0 cache of 180224 rows
+cfg3  prefill M = 2048: activations N(0,1) * s[c], s ~ LogNormal(0, 1) per channel, rounded to bf16 values;
+      positions from 0 or 131072; q8_0 cache of 180224 rows
+cfg4  embedding gather: 248320 x 5120 tables (Q4_K, Q6_K, Q8_0, IQ2_S), fp16 scales in [2^-10, 2^-4];
+      2048 Zipf(1.1) ids + 4 uniform ids
+cfg5  multimodal + GDN, 4099 rows = 3 text + a 64 x 64 image grid (IMRoPE positions t, h, w)
+"""
+from __future__ import annotations
+
+import numpy as np
+
+E = 5120
+FF = 17408
+NQH, NKVH = 24, 4
+KH, HV = 16, 48
+C_CONV = 2 * KH * 128 + HV * 128
+EPS = 1e-6
+N_CTX = 180224
+VOCAB = 248320
+THETA_SCALE = float(np.float32(1e7) ** np.float32(-2.0 / 64))  # powf(rope_base, -2 / rope_dims), src/model.cu:712
+BLOCK = {"q4_k": (144, 256), "q6_k": (210, 256), "q8_0": (34, 32), "iq2_s": (82, 256)}
+D_OFFSETS = {"q4_k": (0, 2), "q6_k": (208,), "q8_0": (0,), "iq2_s": (0,)}  # fp16 scale fields inside a block
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def normal(r, n, std=1.0, mean=0.0):
+    return (r.standard_normal(n) * std + mean).astype(np.float32)
+
+
+def to_bf16_values(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+def cfg1(seed=1):
+    r = rng(seed)
+    x = normal(r, E)
+    x[r.choice(E, 5, replace=False)] *= 50
+    return x, normal(r, E, 0.1, 1.0)
+
+
+def prefill_rows(r, M, n=E):
+    s = np.exp(r.standard_normal(n)).astype(np.float32)
+    return to_bf16_values(r.standard_normal((M, n)).astype(np.float32) * s).reshape(-1)
+
+
+def zipf_ids(r, T, vocab=VOCAB, s=1.1):
+    w = np.arange(1, vocab + 1, dtype=np.float64) ** -s
+    cdf = np.cumsum(w)
+    cdf /= cdf[-1]
+    ranks = np.minimum(np.searchsorted(cdf, r.random(T)), vocab - 1)
+    perm = r.permutation(vocab)
+    return perm[ranks].astype(np.int32)
+
+
+def gather_ids(seed=4, T=2048, U=4, vocab=VOCAB):
+    r = rng(seed)
+    return np.concatenate([zipf_ids(r, T, vocab), r.integers(0, vocab, U).astype(np.int32)])
+
+
+def random_table(r, kind, rows, n):
+    """Random block bytes with every fp16 scale field set to a finite value in [2^-10, 2^-4]."""
+    bb, bv = BLOCK[kind]
+    nblk = rows * (n // bv)
+    t = r.integers(0, 256, nblk * bb, dtype=np.uint8).reshape(nblk, bb)
+    for off in D_OFFSETS[kind]:
+        d = np.exp2(r.uniform(-10, -4, nblk)).astype(np.float16)
+        t[:, off:off + 2] = d.view(np.uint8).reshape(nblk, 2)
+    return t.reshape(-1)
+
+
+def rope3_grid(text_before=3, nx=64, ny=64):
+    """IMRoPE rows as tools/q27_server.cpp:353-369 builds them: text rows t = h = w = p, then the image rows
+    (P, P + i / nx, P + i % nx)."""
+    rows = []
+    p = 0
+    for _ in range(text_before):
+        rows.append((p, p, p))
+        p += 1
+    for i in range(nx * ny):
+        rows.append((p, p + i // nx, p + i % nx))
+    return np.array(rows, np.int32).reshape(-1)

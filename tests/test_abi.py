@@ -1,0 +1,103 @@
+"""The C ABI on the host (no GPU needed): the library loads, exports every symbol include/q27h.h declares, and
+rejects the shapes and arguments the reference launchers reject (src/ops.cu:699,704,724,734; src/prefill.cu:518)
+before anything is enqueued. Also compiles the C++ drop-in header q27/ops.h against the ABI."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "q27h.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(q27h_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(q27):
+    L = q27.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 27
+    for s in syms:
+        assert hasattr(L, s), s
+    assert L.q27h_abi_version() == 1
+
+
+def test_python_binding_covers_the_abi(q27):
+    from qwen27_engine_amd import _lib  # loaded by the q27 fixture
+
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_kv_cache_bytes(q27):
+    # src/attn.cu:890-892: q8 -> nkvh * n_ctx * (256 + 16); f16 -> nkvh * n_ctx * 512
+    assert q27.ops.kv_cache_bytes(4, 180224, True) == 4 * 180224 * 272
+    assert q27.ops.kv_cache_bytes(4, 180224, False) == 4 * 180224 * 512
+    assert q27.ops.kv_cache_bytes(2, 1, True) == 544
+
+
+FAKE = 1 << 20  # an aligned non-null address: the calls below must fail before any use of it
+
+
+@pytest.mark.parametrize("call,code,needle", [
+    (lambda o: o.rmsnorm_q8(FAKE, FAKE, FAKE, FAKE, FAKE, 4096, 4, 1e-6, 0), -1, "n must be 5120"),
+    (lambda o: o.sum_norm_q8(FAKE, FAKE, 5120, 4, FAKE, FAKE, 1e-6, FAKE, FAKE, FAKE, 0), -2, "cross-card"),
+    (lambda o: o.sum_norm_q8(FAKE, FAKE, 5000, 4, None, FAKE, 1e-6, FAKE, FAKE, FAKE, 0), -1, "5120"),
+    (lambda o: o.sum_norm_rows(FAKE, FAKE, 5120, 8, FAKE, FAKE, 1e-6, None, FAKE, FAKE, FAKE, 0), -2, "cross-card"),
+    (lambda o: o.add_norm_rows(FAKE, FAKE, None, 1024, 8, FAKE, 1e-6, None, FAKE, FAKE, FAKE, 0), -1, "5120"),
+    (lambda o: o.swiglu_q8(FAKE, FAKE, FAKE, FAKE, 100, 0), -1, "n % 32"),
+    (lambda o: o.quantize_q8_1(FAKE, FAKE, FAKE, 100, 2, 0), -1, "multiple of 32"),
+    (lambda o: o.gdn_conv_l2(FAKE, FAKE, FAKE, FAKE, FAKE, 10240, 4, True, 32, 1e-6, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 47, 0),
+     -1, "bad shape"),
+    (lambda o: o.gdn_conv_l2(FAKE, FAKE, FAKE, FAKE, FAKE, 10240, 5, True, 32, 1e-6, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 0),
+     -1, "T must be <= 4"),
+    (lambda o: o.gdn_conv_prefill(FAKE, FAKE, FAKE, FAKE, FAKE, 10200, 64, 32, 1e-6, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 0),
+     -1, "bad shape"),
+    (lambda o: o.get_rows_q4_k(FAKE, 2880, FAKE, 4, FAKE, 5000, 0), -1, "multiple of 256"),
+    (lambda o: o.get_rows_q8_0(FAKE, 100, FAKE, 4, FAKE, 5120, 0), -1, "row_bytes"),
+    (lambda o: o.rmsnorm_q8(FAKE + 4, FAKE, None, FAKE, FAKE, 5120, 4, 1e-6, 0), -4, "alignment"),
+    (lambda o: o.attn_prep(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 1e-6, 0.6, 24, 4, 0, True, 0), -1, "bad shape"),
+])
+def test_rejected_before_launch(q27, call, code, needle):
+    with pytest.raises(q27.Q27Error) as ei:
+        call(q27.ops)
+    assert ei.value.code == code
+    assert needle in str(ei.value)
+
+
+def test_empty_inputs_are_no_ops(q27):
+    # zero rows / tokens enqueue nothing (and so need no device)
+    q27.ops.rmsnorm_q8(FAKE, FAKE, None, FAKE, FAKE, 5120, 0, 1e-6, 0)
+    q27.ops.swiglu_q8(FAKE, FAKE, FAKE, FAKE, 0, 0)
+    q27.ops.gated_rmsnorm_q8(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1e-6, 0)
+    q27.ops.get_rows_iq2_s(FAKE, 1640, FAKE, 0, FAKE, 5120, 0)
+    q27.ops.attn_prep(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1e-6, 0.6, 24, 4, 16, True, 0)
+
+
+def test_cpp_dropin_header_compiles(tmp_path):
+    """include/q27/ops.h re-exposes the reference signatures; a caller written against src/ops.h compiles."""
+    src = tmp_path / "caller.cpp"
+    src.write_text(r'''
+#include "q27/ops.h"
+#include "q27/prefill.h"
+#include "q27/qmat.h"
+void step(float* x, const float* part, const float* w, float* h, int8_t* xq, float* xd, float* xs, hipStream_t s,
+          const float* g, const float* u, const uint8_t* emb, const int* ids, int* plane) {
+  q27::rmsnorm_q8(x, w, h, xq, xd, 5120, 4, 1e-6f, s);
+  q27::sum_norm_q8(x, part, 5120, 4, nullptr, w, 1e-6f, h, xq, xd, s);
+  q27::swiglu_q8(g, u, xq, xd, 4 * 17408, s);
+  q27::sum_norm_rows(x, part, 5120, 2048, nullptr, w, 1e-6f, nullptr, xq, xd, xs, s);
+  q27::quantize_q8_1(x, xq, xd, 6144, 2048, s, xs);
+  q27::get_rows_iq2_s(emb, 1640, ids, 4, x, 5120, s);
+  q27::gdn_flip_plane(plane, s);
+  (void)q27::kv_cache_bytes(4, 180224, true);
+}
+''')
+    inc = os.path.join(ROOT, "include")
+    r = subprocess.run(["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{inc}", "-I/opt/rocm/include",
+                        str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
