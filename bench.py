@@ -298,6 +298,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-rows", type=int, default=128)
     ap.add_argument("--calib-copy", action="store_true", help="also run a plain 256 MiB copy (rocprof counter calibration)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the fused-op path has no multi-GPU form in this build "
@@ -330,6 +332,17 @@ def main():
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"prefill: {ms_per_step * 1e3:.1f} us per 2048-token batch, {value:.0f} GB/s")
+    if args.prefill_only:
+        if args.calib_copy:
+            src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            log("calibration copy: 3 x 256 MiB device-to-device")
+        print(json.dumps({"metric": "prefill-only profiling run", "value": round(value, 1), "unit": "GB/s",
+                          "ms_per_step": round(ms_per_step, 4)}), flush=True)
+        return
 
     # ---- per-op breakdown inside the pass (HIP events around each launch)
     acc = {}
@@ -342,11 +355,41 @@ def main():
         per_op[name] = {"us": round(us, 2), "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
                         "bytes": b // cnt, "launches_per_step": cnt // max(1, min(3, args.steps))}
         log(f"  {name:18s} {us:9.2f} us  {gbs:8.1f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
-    dom = per_op["swiglu_q8"]
-    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "swiglu_q8 (flat_q8_kernel<true>)",
-                "bytes_per_launch": dom["bytes"], "avg_launch_us": dom["us"]}
-    del P
+    # ---- roofline of the dominant kernel (swiglu_q8 at M = 2048): back-to-back launches between two HIP events
+    # on the stream the kernel runs on (torch's current stream, which the launchers use)
+    # Three input sets are cycled (3 x 285 MB of g, u) so no launch finds its inputs in the 256 MB MALL.
+    n_sw = 2048 * FF
+    sw_bytes = bytes_swiglu_q8(n_sw, True)
+    sets = [(P.fg, P.fu)] + [(torch.randn(n_sw, device="cuda") * 2, torch.randn(n_sw, device="cuda") * 2) for _ in range(2)]
+    for i in range(3):
+        q27.ops.swiglu_q8(sets[i][0], sets[i][1], P.xq, P.xd, n_sw, None, P.xs)
+    reps = 21
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(reps):
+        q27.ops.swiglu_q8(sets[i % 3][0], sets[i % 3][1], P.xq, P.xd, n_sw, None, P.xs)
+    b.record()
+    torch.cuda.synchronize()
+    sw_us = a.elapsed_time(b) * 1e3 / reps
+    sw_gbs = sw_bytes / (sw_us * 1e-6) / 1e9
+    log(f"swiglu_q8 back-to-back: {sw_us:.2f} us per launch, {sw_gbs:.0f} GB/s")
+    roofline = {"bound": "hbm", "achieved": round(sw_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(sw_gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "swiglu_q8 (flat_q8_kernel<true>)",
+                "bytes_per_launch": sw_bytes, "avg_launch_us": round(sw_us, 2),
+                "note": "2048 x 17408 values, 9.375 B each (g, u f32 in; xq int8, xd f32 per 32, xs f32 per 16 out)"}
+    # ---- practical copy ceiling of this device (torch device-to-device copy of 512 MiB, read + write bytes)
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    a.record()
+    for _ in range(10):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * (512 << 20) * 10 / (a.elapsed_time(b) * 1e-3) / 1e9
+    log(f"device copy ceiling: {copy_gbs:.0f} GB/s")
+    del src, dst, P, sets
     torch.cuda.empty_cache()
 
     # ---- decode verify pass (T = 4) in one HIP graph
@@ -400,6 +443,7 @@ def main():
                                "(48 GDN + 16 attention), q8_0 KV cache of 180224 rows, IQ2_S embedding",
                    "tokens": 2048, "layers": N_LAYER, "launches_per_step": len(acc) and sum(v["launches_per_step"] for v in per_op.values())},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "copy_ceiling_GBps": round(copy_gbs, 1),
         "us_per_2048_batch": round(ms_per_step * 1e3, 1),
         "decode_us_per_step": round(decode_us, 1),
         "per_op": per_op,

@@ -1,7 +1,7 @@
 // Attention input stage (attn_prep): per-head RMSNorm of q and k, partial NeoX rotary (plain positions or
 // IMRoPE sections), and the K/V cache write as f16 or q8_0.
 //
-// One wave per (token, head), lane p holding head dims 4p .. 4p+3 (16-byte loads and stores). The reference's
+// Lane p of a wave holds head dims 4p .. 4p+3 (16-byte loads and stores). The reference's
 // 256-thread block_sum (src/ops.cu:609) is rebuilt from the same operands: per virtual warp of 32 dims
 // (8 lanes) vwarp_sum4, then the second stage over the 8 warp sums w_g (lanes 8g..8g+7), whose reference tree
 // ((w0+w4)+(w2+w6)) + ((w1+w5)+(w3+w7)) is lane xor 32, xor 16, xor 8. The rotary partner of dim j < 32 is dim
@@ -19,6 +19,12 @@ struct RopeFreqs {
   float f[32];
 };
 
+
+// One wave per (token, group of HPW consecutive heads): HPW = 4 for batches (the 28 heads of a token are 7 waves),
+// HPW = 1 for a few tokens, where the shorter chain per wave matters more than loads in flight. The 32 rotary angles of the token are evaluated
+// once per wave (lane j < 32 takes pair j) and handed to the lanes that need them with ds_bpermute; the head
+// vectors of the whole group are loaded before any arithmetic.
+template <int HPW>
 __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict__ qg, const float* __restrict__ k,
                                                         const float* __restrict__ v, const float* __restrict__ q_norm,
                                                         const float* __restrict__ k_norm, float* __restrict__ qn,
@@ -27,91 +33,121 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
                                                         int nqh, int nkvh, int n_ctx, int q8, const int* __restrict__ rope3,
                                                         const int* __restrict__ rdelta) {
   const int nh = nqh + nkvh;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= T * nh) return;  // whole waves leave together
-  const int tok = item / nh, hb = item % nh;
+  const int wpt = (nh + HPW - 1) / HPW;  // waves per token
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave >= T * wpt) return;  // whole waves leave together
+  const int tok = wave / wpt;
+  const int hb0 = (wave % wpt) * HPW;
+  const int nhw = min(HPW, nh - hb0);
   const int p = threadIdx.x & 63;
   const int pos = *dpos0 + tok;  // cache row
-  const bool isq = hb < nqh;
-  const float* src = isq ? qg + (size_t)tok * nqh * 512 + (size_t)hb * 512 : k + ((size_t)tok * nkvh + (hb - nqh)) * 256;
-  const float* w = isq ? q_norm : k_norm;
-  const float4 xv = ld4(src + 4 * p);
-  const float x[4] = {xv.x, xv.y, xv.z, xv.w};
-  float s[4];
+  // ---- loads of the whole group
+  float4 xin[HPW], vin[HPW];
 #pragma unroll
-  for (int c = 0; c < 4; c++) s[c] = x[c] * x[c];
-  float t = vwarp_sum4(s);
-  t = t + lane_xor32(t);
-  t += lane_xor<16>(t);
-  t += lane_xor<8>(t);
-  const float scale = 1.0f / __builtin_sqrtf(t / 256.0f + eps);
-  const float4 wv = ld4(w + 4 * p);
-  const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
-  float buf[4], out[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    buf[c] = scale * x[c] * ww[c];
-    out[c] = buf[c];
-  }
-  float partner[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) partner[c] = lane_xor<8>(buf[c]);
-  if (p < 16) {
-    const int plain = pos - (rdelta ? *rdelta : 0);
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const int j = (4 * p + c) & 31;
-      const int rp = rope3 ? rope3[tok * 3 + j % 3] : plain;
-      const float theta = (float)rp * fr.f[j];
-      float sn, cs;
-      q27_sincos(theta, &sn, &cs);
-      if (p < 8) out[c] = buf[c] * cs - partner[c] * sn;  // x0 * c - x1 * s, x0 = dim j, x1 = dim j + 32
-      else out[c] = partner[c] * sn + buf[c] * cs;        // x0 * s + x1 * c
+  for (int i = 0; i < HPW; i++) {
+    const int hb = hb0 + i;
+    if (i < nhw) {
+      if (hb < nqh) {
+        xin[i] = ld4(qg + ((size_t)tok * nqh + hb) * 512 + 4 * p);
+      } else {
+        const size_t off = ((size_t)tok * nkvh + (hb - nqh)) * 256 + 4 * p;
+        xin[i] = ld4(k + off);
+        vin[i] = ld4(v + off);
+      }
     }
   }
-  if (isq) {
-    st4(qn + ((size_t)tok * nqh + hb) * 256 + 4 * p, out[0], out[1], out[2], out[3]);
-    return;
+  const float4 qw = ld4(q_norm + 4 * p);
+  const float4 kw = nkvh ? ld4(k_norm + 4 * p) : qw;
+  // ---- rotary angles of the token: lane j < 32 evaluates pair j
+  float sn_j = 0.0f, cs_j = 1.0f;
+  if (p < 32) {
+    const int rp = rope3 ? rope3[tok * 3 + p % 3] : pos - (rdelta ? *rdelta : 0);
+    q27_sincos((float)rp * fr.f[p], &sn_j, &cs_j);
   }
-  const int kh = hb - nqh;
-  const float4 vvv = ld4(v + ((size_t)tok * nkvh + kh) * 256 + 4 * p);
-  const float vv[4] = {vvv.x, vvv.y, vvv.z, vvv.w};
+  float snc[4], csc[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int j = (4 * p + c) & 31;
+    snc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, sn_j)));
+    csc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, cs_j)));
+  }
   const bool valid = pos >= 0 && pos < n_ctx;  // uniform over the wave
-  const size_t row = (size_t)kh * n_ctx + (size_t)(valid ? pos : 0);
-  if (!q8) {
-    if (!valid) return;
-    uint16_t* kc = (uint16_t*)kcache + row * 256 + 4 * p;
-    uint16_t* vc = (uint16_t*)vcache + row * 256 + 4 * p;
-    *(uint2*)kc = make_uint2((uint32_t)f2h_bits(out[0]) | ((uint32_t)f2h_bits(out[1]) << 16),
-                             (uint32_t)f2h_bits(out[2]) | ((uint32_t)f2h_bits(out[3]) << 16));
-    *(uint2*)vc = make_uint2((uint32_t)f2h_bits(vv[0]) | ((uint32_t)f2h_bits(vv[1]) << 16),
-                             (uint32_t)f2h_bits(vv[2]) | ((uint32_t)f2h_bits(vv[3]) << 16));
-    return;
-  }
-  // q8_0 per 32 dims (8 lanes): d = amax / 127, q = roundf(x * (d ? 1/d : 0)) (src/ops.cu:636-646)
-  float ak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(out[0]), __builtin_fabsf(out[1])),
-                             __builtin_fmaxf(__builtin_fabsf(out[2]), __builtin_fabsf(out[3])));
-  float av = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(vv[0]), __builtin_fabsf(vv[1])),
-                             __builtin_fmaxf(__builtin_fabsf(vv[2]), __builtin_fabsf(vv[3])));
-  ak = __builtin_fmaxf(ak, lane_xor<4>(ak));
-  av = __builtin_fmaxf(av, lane_xor<4>(av));
-  ak = __builtin_fmaxf(ak, lane_xor<2>(ak));
-  av = __builtin_fmaxf(av, lane_xor<2>(av));
-  ak = __builtin_fmaxf(ak, lane_xor<1>(ak));
-  av = __builtin_fmaxf(av, lane_xor<1>(av));
-  if (!valid) return;
-  const float dk = ak / 127.f, dv = av / 127.f;
-  const float ik = dk != 0.0f ? 1.0f / dk : 0.0f, iv = dv != 0.0f ? 1.0f / dv : 0.0f;
-  int8_t* kq = (int8_t*)kcache + row * 256 + 4 * p;
-  int8_t* vq = (int8_t*)vcache + row * 256 + 4 * p;
-  *(uint32_t*)kq = pack4_i8((int)__builtin_roundf(out[0] * ik), (int)__builtin_roundf(out[1] * ik),
-                            (int)__builtin_roundf(out[2] * ik), (int)__builtin_roundf(out[3] * ik));
-  *(uint32_t*)vq = pack4_i8((int)__builtin_roundf(vv[0] * iv), (int)__builtin_roundf(vv[1] * iv),
-                            (int)__builtin_roundf(vv[2] * iv), (int)__builtin_roundf(vv[3] * iv));
-  if ((p & 7) == 0) {
-    const size_t so = (size_t)nkvh * n_ctx * 256;
-    ((uint16_t*)((uint8_t*)kcache + so))[row * 8 + (p >> 3)] = f2h_bits(dk);
-    ((uint16_t*)((uint8_t*)vcache + so))[row * 8 + (p >> 3)] = f2h_bits(dv);
+  const size_t so = (size_t)nkvh * n_ctx * 256;
+#pragma unroll
+  for (int i = 0; i < HPW; i++) {
+    if (i >= nhw) break;
+    const int hb = hb0 + i;
+    const bool isq = hb < nqh;
+    const float x[4] = {xin[i].x, xin[i].y, xin[i].z, xin[i].w};
+    // RMSNorm over the 256 dims: 8 virtual warps of 32 (8 lanes each), then ((w0+w4)+(w2+w6)) + ((w1+w5)+(w3+w7))
+    float s[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) s[c] = x[c] * x[c];
+    float t = vwarp_sum4(s);
+    t = t + lane_xor32(t);
+    t += lane_xor<16>(t);
+    t += lane_xor<8>(t);
+    const float scale = 1.0f / __builtin_sqrtf(t / 256.0f + eps);
+    const float4 wv = isq ? qw : kw;
+    const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    float buf[4], out[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      buf[c] = scale * x[c] * ww[c];
+      out[c] = buf[c];
+    }
+    // NeoX rotation of (j, j + 32), j < 32: the partner of lane p < 16 is lane p ^ 8
+    float partner[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) partner[c] = lane_xor<8>(buf[c]);
+    if (p < 8) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) out[c] = buf[c] * csc[c] - partner[c] * snc[c];   // x0 * c - x1 * s
+    } else if (p < 16) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) out[c] = partner[c] * snc[c] + buf[c] * csc[c];   // x0 * s + x1 * c
+    }
+    if (isq) {
+      st4(qn + ((size_t)tok * nqh + hb) * 256 + 4 * p, out[0], out[1], out[2], out[3]);
+      continue;
+    }
+    const int kh = hb - nqh;
+    const float vv[4] = {vin[i].x, vin[i].y, vin[i].z, vin[i].w};
+    const size_t row = (size_t)kh * n_ctx + (size_t)(valid ? pos : 0);
+    if (!q8) {
+      if (!valid) continue;
+      uint16_t* kc = (uint16_t*)kcache + row * 256 + 4 * p;
+      uint16_t* vc = (uint16_t*)vcache + row * 256 + 4 * p;
+      *(uint2*)kc = make_uint2((uint32_t)f2h_bits(out[0]) | ((uint32_t)f2h_bits(out[1]) << 16),
+                               (uint32_t)f2h_bits(out[2]) | ((uint32_t)f2h_bits(out[3]) << 16));
+      *(uint2*)vc = make_uint2((uint32_t)f2h_bits(vv[0]) | ((uint32_t)f2h_bits(vv[1]) << 16),
+                               (uint32_t)f2h_bits(vv[2]) | ((uint32_t)f2h_bits(vv[3]) << 16));
+      continue;
+    }
+    // q8_0 per 32 dims (8 lanes): d = amax / 127, q = roundf(x * (d ? 1/d : 0)) (src/ops.cu:636-646)
+    float ak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(out[0]), __builtin_fabsf(out[1])),
+                               __builtin_fmaxf(__builtin_fabsf(out[2]), __builtin_fabsf(out[3])));
+    float av = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(vv[0]), __builtin_fabsf(vv[1])),
+                               __builtin_fmaxf(__builtin_fabsf(vv[2]), __builtin_fabsf(vv[3])));
+    ak = __builtin_fmaxf(ak, lane_xor<4>(ak));
+    av = __builtin_fmaxf(av, lane_xor<4>(av));
+    ak = __builtin_fmaxf(ak, lane_xor<2>(ak));
+    av = __builtin_fmaxf(av, lane_xor<2>(av));
+    ak = __builtin_fmaxf(ak, lane_xor<1>(ak));
+    av = __builtin_fmaxf(av, lane_xor<1>(av));
+    if (!valid) continue;
+    const float dk = ak / 127.f, dv = av / 127.f;
+    const float ik = dk != 0.0f ? 1.0f / dk : 0.0f, iv = dv != 0.0f ? 1.0f / dv : 0.0f;
+    int8_t* kq = (int8_t*)kcache + row * 256 + 4 * p;
+    int8_t* vq = (int8_t*)vcache + row * 256 + 4 * p;
+    *(uint32_t*)kq = pack4_i8((int)__builtin_roundf(out[0] * ik), (int)__builtin_roundf(out[1] * ik),
+                              (int)__builtin_roundf(out[2] * ik), (int)__builtin_roundf(out[3] * ik));
+    *(uint32_t*)vq = pack4_i8((int)__builtin_roundf(vv[0] * iv), (int)__builtin_roundf(vv[1] * iv),
+                              (int)__builtin_roundf(vv[2] * iv), (int)__builtin_roundf(vv[3] * iv));
+    if ((p & 7) == 0) {
+      ((uint16_t*)((uint8_t*)kcache + so))[row * 8 + (p >> 3)] = f2h_bits(dk);
+      ((uint16_t*)((uint8_t*)vcache + so))[row * 8 + (p >> 3)] = f2h_bits(dv);
+    }
   }
 }
 
@@ -139,8 +175,15 @@ extern "C" int q27h_attn_prep(const float* qg, const float* k, const float* v, c
     return fail(Q27H_ERR_ARG, "attn_prep: tensors need 16-byte alignment");
   RopeFreqs fr;
   for (int j = 0; j < 32; j++) fr.f[j] = powf(theta_scale, (float)j);
-  const long items = (long)T * (nqh + nkvh);
-  hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm, k_norm,
-                     qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
+  const int nh = nqh + nkvh;
+  if ((long)T * nh < 2048) {
+    const long waves = (long)T * nh;
+    hipLaunchKernelGGL(attn_prep_kernel<1>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm,
+                       k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
+  } else {
+    const long waves = (long)T * ((nh + 3) / 4);
+    hipLaunchKernelGGL(attn_prep_kernel<4>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm,
+                       k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
+  }
   return check_launch("attn_prep");
 }

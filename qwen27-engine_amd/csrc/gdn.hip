@@ -10,6 +10,13 @@
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
+#ifndef Q27H_GDN_PRELOAD
+#define Q27H_GDN_PRELOAD 0
+#endif
+#ifndef Q27H_GDN_CH
+#define Q27H_GDN_CH 16
+#endif
+
 namespace q27h {
 namespace {
 
@@ -50,21 +57,28 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
   g[i] = q27_softplus(a[i] + dt_bias[hv]) * ssm_a[hv];
 }
 
-template <bool PREFILL>
+template <bool PREFILL, int CH>
 __global__ void __launch_bounds__(256) gdn_conv_fused_kernel(const float* __restrict__ x, const float* __restrict__ cw,
                                                              float* __restrict__ planes, const int* __restrict__ in_plane,
                                                              float* __restrict__ y, int C, int T, int snapshots,
                                                              int n_norm_heads, float eps, const float* __restrict__ a,
                                                              const float* __restrict__ b, const float* __restrict__ ssm_a,
                                                              const float* __restrict__ dt_bias, float* __restrict__ g,
-                                                             float* __restrict__ beta, int H, int chunk, int nchunks) {
+                                                             float* __restrict__ beta, int H, int nchunks) {
   const int nheads = C / 128;
   const int item = blockIdx.x * 8 + (threadIdx.x >> 5);
   if (item >= nheads * nchunks) return;  // whole halves leave together
-  const int head = item / nchunks, ch = item % nchunks;
+  const int head = item % nheads, ch = item / nheads;  // neighbouring halves: neighbouring heads of one token range
   const int p = threadIdx.x & 31;
   const int c0 = head * 128 + 4 * p;
-  const int t0 = ch * chunk, t1 = min(T, t0 + chunk);
+  const int t0 = ch * CH, t1 = min(T, t0 + CH);
+#if Q27H_GDN_PRELOAD
+  // every input row of the chunk is loaded before the first token is processed
+  float4 xr[CH];
+#pragma unroll
+  for (int i = 0; i < CH; i++)
+    if (t0 + i < t1) xr[i] = ld4(x + (size_t)(t0 + i) * C + c0);
+#endif
   const int pin = *in_plane;
   float w[4][4];
 #pragma unroll
@@ -89,9 +103,16 @@ __global__ void __launch_bounds__(256) gdn_conv_fused_kernel(const float* __rest
     }
   }
   const bool norm = head < n_norm_heads;
-  for (int t = t0; t < t1; t++) {
+#pragma unroll
+  for (int i = 0; i < CH; i++) {
+    const int t = t0 + i;
+    if (t >= t1) break;
+#if Q27H_GDN_PRELOAD
+    const float xn[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+#else
     const float4 xv = ld4(x + (size_t)t * C + c0);
     const float xn[4] = {xv.x, xv.y, xv.z, xv.w};
+#endif
     float out[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -220,8 +241,8 @@ extern "C" int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, c
   if (T > 4) return fail(Q27H_ERR_SHAPE, "gdn_conv_l2: T must be <= 4 (4 state planes)");
   if (T == 0) return Q27H_OK;
   const int items = C / 128;
-  hipLaunchKernelGGL(gdn_conv_fused_kernel<false>, dim3((items + 7) / 8), dim3(256), 0, stream_of(s), x, w, planes, in_plane,
-                     y, C, T, snapshots, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, T, 1);
+  hipLaunchKernelGGL((gdn_conv_fused_kernel<false, 4>), dim3((items + 7) / 8), dim3(256), 0, stream_of(s), x, w, planes,
+                     in_plane, y, C, T, snapshots, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, 1);
   return check_launch("gdn_conv_l2");
 }
 
@@ -231,11 +252,11 @@ extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* plan
   if (int e = check_fused("gdn_conv_prefill", x, w, planes, in_plane, y, C, M, n_norm_heads, H, a, b, ssm_a, dt_bias, g, beta))
     return e;
   if (M == 0) return Q27H_OK;
-  const int chunk = 16;  // tokens per half-wave; >= 3 so a chunk's window never reaches past the previous chunk
+  constexpr int chunk = Q27H_GDN_CH;  // tokens per half-wave; >= 3 so a chunk's window never reaches past the previous chunk
   const int nchunks = (M + chunk - 1) / chunk;
   const long items = (long)(C / 128) * nchunks;
-  hipLaunchKernelGGL(gdn_conv_fused_kernel<true>, dim3((unsigned)((items + 7) / 8)), dim3(256), 0, stream_of(s), x, w, planes,
-                     in_plane, y, C, M, 0, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, chunk, nchunks);
+  hipLaunchKernelGGL((gdn_conv_fused_kernel<true, chunk>), dim3((unsigned)((items + 7) / 8)), dim3(256), 0, stream_of(s), x, w,
+                     planes, in_plane, y, C, M, 0, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, nchunks);
   return check_launch("gdn_conv_prefill");
 }
 

@@ -1,9 +1,9 @@
 // Quantized embedding gather: rows of a GGUF-block table (IQ2_S, Q4_K, Q6_K, Q8_0) -> f32 [T][n]; an id < 0
 // copies a row of the image-embedding array instead (src/ops.cu:343-375).
 //
-// One 256-thread workgroup per (token, 1024-value chunk): the chunk's compressed bytes (<= 1088) are first
-// staged in LDS with coalesced dword loads, then each thread decodes 4 consecutive values and writes them as one
-// 16-byte store. Dequantization follows ggml's float order (the reference's IQ2_S kernel and its host
+// One 256-thread workgroup per (token, 5120-value chunk, i.e. one row of the model): the chunk's compressed bytes
+// (<= 5440) are first staged in LDS with coalesced dword loads, then each thread decodes groups of 4 consecutive
+// values and writes each group as one 16-byte store. Dequantization follows ggml's float order (the reference's IQ2_S kernel and its host
 // transcriptions of Q4_K / Q6_K in src/requant.cpp:68-114).
 #include "q27h_device.h"
 #include "q27h_internal.h"
@@ -16,7 +16,7 @@ __constant__ uint64_t c_iq2s_grid[1024] = {
 };
 
 enum Fmt { kIQ2S = 0, kQ4K = 1, kQ6K = 2, kQ80 = 3 };
-constexpr int kChunk = 1024;
+constexpr int kChunk = 5120;  // values per workgroup: one embedding row of the 27B model
 
 template <int F>
 struct FmtInfo;
@@ -105,10 +105,10 @@ __global__ void __launch_bounds__(256) get_rows_kernel(const uint8_t* __restrict
   const int id = ids[tok];
   float* out = y + (size_t)tok * n + v0;
   if (id < 0) {
-    if (4 * t < nv) {
+    for (int o = 4 * t; o < nv; o += 1024) {
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (img) a = ld4(img + (size_t)(-id - 1) * n + v0 + 4 * t);
-      *(float4*)(out + 4 * t) = a;
+      if (img) a = ld4(img + (size_t)(-id - 1) * n + v0 + o);
+      *(float4*)(out + o) = a;
     }
     return;
   }
@@ -122,11 +122,11 @@ __global__ void __launch_bounds__(256) get_rows_kernel(const uint8_t* __restrict
     for (int i = t; i < nbytes; i += 256) sb[i] = src[i];
   }
   __syncthreads();
-  if (4 * t >= nv) return;
-  const int o = 4 * t;
-  float v[4];
-  decode4<F>((const uint8_t*)stage + (o / BV) * BB, o % BV, v);
-  *(float4*)(out + o) = make_float4(v[0], v[1], v[2], v[3]);
+  for (int o = 4 * t; o < nv; o += 1024) {
+    float v[4];
+    decode4<F>((const uint8_t*)stage + (o / BV) * BB, o % BV, v);
+    *(float4*)(out + o) = make_float4(v[0], v[1], v[2], v[3]);
+  }
 }
 
 template <int F>

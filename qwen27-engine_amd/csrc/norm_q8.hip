@@ -27,11 +27,14 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   const size_t row = blockIdx.x;
   const size_t base = row * kRowN + 4 * t;
   float v[5][4];
+  float4 wv[5];
 #pragma unroll
   for (int k = 0; k < 5; k++) {
     const float4 a = ld4(x + base + k * 1024);
     v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
   }
+#pragma unroll
+  for (int k = 0; k < 5; k++) wv[k] = ld4(w + 4 * t + k * 1024);  // issued before the reduction: no extra round trip
   if constexpr (MODE != kPlain) {
 #pragma unroll
     for (int k = 0; k < 5; k++) {
@@ -66,8 +69,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   const float scale = 1.0f / __builtin_sqrtf(tot / (float)kRowN + eps);
 #pragma unroll
   for (int k = 0; k < 5; k++) {
-    const float4 wv = ld4(w + 4 * t + k * 1024);
-    const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const float ww[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
     float y[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) y[c] = scale * v[k][c] * ww[c];
@@ -77,54 +79,137 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 }
 
 // ---------------------------------------------------------------- flat q8_1 producers
-// Thread i handles values 4i .. 4i+3 of a flat array (n % 32 == 0, so a q8 block is 8 aligned lanes).
+// A 256-thread workgroup covers kFlatU * 1024 consecutive values; thread t handles values 4t .. 4t+3 of each
+// 1024-value chunk (n % 32 == 0, so a q8 block is 8 aligned lanes of one chunk). All loads of a thread are
+// issued before any arithmetic so kFlatU * 16 (quantize) or 32 (swiglu) bytes per lane are in flight.
+#ifndef Q27H_PERSIST
+#define Q27H_PERSIST 0
+#endif
+#ifndef Q27H_FLAT_U
+#define Q27H_FLAT_U 2
+#endif
+constexpr int kFlatU = Q27H_FLAT_U;
+
 template <bool SWIGLU>
 __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                       int8_t* __restrict__ xq, float* __restrict__ xd,
                                                       float* __restrict__ xs, size_t n) {
-  const size_t i0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i0 >= n) return;  // whole 8-lane groups leave together
-  const float4 a = ld4(g + i0);
-  float y[4] = {a.x, a.y, a.z, a.w};
-  if constexpr (SWIGLU) {
-    const float4 b = ld4(u + i0);
-    const float ub[4] = {b.x, b.y, b.z, b.w};
+  const size_t base = (size_t)blockIdx.x * (kFlatU * 1024) + 4 * threadIdx.x;
+  float4 a[kFlatU], b[kFlatU];
 #pragma unroll
-    for (int c = 0; c < 4; c++) y[c] = q27_silu(y[c]) * ub[c];
+  for (int c = 0; c < kFlatU; c++) {
+    const size_t i0 = base + (size_t)c * 1024;
+    if (i0 < n) {
+      a[c] = ld4_nt(g + i0);
+      if constexpr (SWIGLU) b[c] = ld4_nt(u + i0);
+    }
   }
-  q8_1_store4(y, xq, xd, xs, i0);
+#pragma unroll
+  for (int c = 0; c < kFlatU; c++) {
+    const size_t i0 = base + (size_t)c * 1024;
+    if (i0 >= n) break;  // whole 8-lane groups leave together
+    float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
+    if constexpr (SWIGLU) {
+      const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) y[k] = q27_silu(y[k]) * ub[k];
+    }
+    q8_1_store4(y, xq, xd, xs, i0);
+  }
+}
+
+// Persistent form: gridDim.x workgroups walk the kFlatU * 1024-value tiles with stride gridDim.x, and the loads of
+// the next tile are issued before the current tile is computed (one tile of prefetch per thread).
+template <bool SWIGLU>
+__global__ void __launch_bounds__(256) flat_q8_persist_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                              int8_t* __restrict__ xq, float* __restrict__ xd,
+                                                              float* __restrict__ xs, size_t n, size_t ntiles) {
+  float4 a[kFlatU], b[kFlatU], na[kFlatU], nb[kFlatU];
+  size_t tile = blockIdx.x;
+  auto load = [&](size_t tl, float4 (&ra)[kFlatU], float4 (&rb)[kFlatU]) {
+    const size_t base = tl * (kFlatU * 1024) + 4 * threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < kFlatU; c++) {
+      const size_t i0 = base + (size_t)c * 1024;
+      if (i0 < n) {
+        ra[c] = ld4_nt(g + i0);
+        if constexpr (SWIGLU) rb[c] = ld4_nt(u + i0);
+      }
+    }
+  };
+  if (tile < ntiles) load(tile, a, b);
+  for (; tile < ntiles; tile += gridDim.x) {
+    const size_t next = tile + gridDim.x;
+    if (next < ntiles) load(next, na, nb);
+    const size_t base = tile * (kFlatU * 1024) + 4 * threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < kFlatU; c++) {
+      const size_t i0 = base + (size_t)c * 1024;
+      if (i0 >= n) break;  // whole 8-lane groups leave together
+      float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
+      if constexpr (SWIGLU) {
+        const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) y[k] = q27_silu(y[k]) * ub[k];
+      }
+      q8_1_store4(y, xq, xd, xs, i0);
+    }
+#pragma unroll
+    for (int c = 0; c < kFlatU; c++) {
+      a[c] = na[c];
+      if constexpr (SWIGLU) b[c] = nb[c];
+    }
+  }
 }
 
 // ---------------------------------------------------------------- gated RMSNorm -> q8_1 (heads of 128)
-// 32 lanes per head, lane p holds values 4p .. 4p+3; a 256-thread workgroup covers 8 heads. The reference's
-// 128-thread block_sum (4 warps) becomes: per virtual warp (8 lanes) vwarp_sum4, then the second stage over 4
-// warp sums with zeros in lanes 4..31, i.e. (w0 + w2) + (w1 + w3) = lane xor 16, then lane xor 8.
+// 32 lanes per head, lane p holds values 4p .. 4p+3; each 32-lane half handles kGatedH consecutive heads (loads
+// of all of them issued first), a 256-thread workgroup 8 * kGatedH heads. The reference's 128-thread block_sum
+// (4 warps) becomes: per virtual warp (8 lanes) vwarp_sum4, then the second stage over the 4 warp sums with
+// zeros in lanes 4..31, i.e. (w0 + w2) + (w1 + w3) = lane xor 16, then lane xor 8.
+#ifndef Q27H_GATED_H
+#define Q27H_GATED_H 1
+#endif
+constexpr int kGatedH = Q27H_GATED_H;
+
 __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __restrict__ o, const float* __restrict__ w,
                                                                const float* __restrict__ z, int8_t* __restrict__ xq,
                                                                float* __restrict__ xd, float eps, float* __restrict__ xs,
                                                                int heads) {
-  const int head = blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (head >= heads) return;  // whole 32-lane halves leave together
+  const int head0 = (blockIdx.x * 8 + (threadIdx.x >> 5)) * kGatedH;
+  if (head0 >= heads) return;  // whole 32-lane halves leave together
   const int p = threadIdx.x & 31;
-  const size_t i0 = (size_t)head * 128 + 4 * p;
-  const float4 ov = ld4(o + i0);
-  const float v[4] = {ov.x, ov.y, ov.z, ov.w};
-  float s[4];
+  const int nh = min(kGatedH, heads - head0);
+  float4 ov[kGatedH], zv[kGatedH];
 #pragma unroll
-  for (int c = 0; c < 4; c++) s[c] = v[c] * v[c];
-  float tsum = vwarp_sum4(s);
-  tsum = tsum + 0.0f;  // the reference adds the zero lanes 4..31 (xor 16, 8, 4 steps); x + 0 == x for x >= +0
-  tsum += lane_xor<16>(tsum);
-  tsum += lane_xor<8>(tsum);
-  const float scale = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
+  for (int k = 0; k < kGatedH; k++) {
+    if (k < nh) {
+      const size_t i0 = (size_t)(head0 + k) * 128 + 4 * p;
+      ov[k] = ld4_nt(o + i0);
+      zv[k] = ld4_nt(z + i0);
+    }
+  }
   const float4 wv = ld4(w + 4 * p);
-  const float4 zv = ld4(z + i0);
   const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
-  const float zz[4] = {zv.x, zv.y, zv.z, zv.w};
-  float y[4];
 #pragma unroll
-  for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * q27_silu(zz[c]);
-  q8_1_store4(y, xq, xd, xs, i0);
+  for (int k = 0; k < kGatedH; k++) {
+    if (k >= nh) break;
+    const size_t i0 = (size_t)(head0 + k) * 128 + 4 * p;
+    const float v[4] = {ov[k].x, ov[k].y, ov[k].z, ov[k].w};
+    float s[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) s[c] = v[c] * v[c];
+    float tsum = vwarp_sum4(s);
+    tsum = tsum + 0.0f;  // the reference adds the zero lanes 4..31 (xor 16, 8, 4 steps); x + 0 == x for x >= +0
+    tsum += lane_xor<16>(tsum);
+    tsum += lane_xor<8>(tsum);
+    const float scale = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
+    const float zz[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
+    float y[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * q27_silu(zz[c]);
+    q8_1_store4(y, xq, xd, xs, i0);
+  }
 }
 
 // ---------------------------------------------------------------- unfused twins (reference structure)
@@ -197,11 +282,19 @@ int launch_flat(const char* fn, bool swiglu, const float* g, const float* u, int
   if (!g || !xq || !xd || (swiglu && !u)) return fail(Q27H_ERR_ARG, std::string(fn) + ": null pointer");
   if (!aligned16(g) || (swiglu && !aligned16(u)) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, std::string(fn) + ": inputs need 16-byte and xq 4-byte alignment");
-  const size_t blocks = (n / 4 + 255) / 256;
+  const size_t blocks = (n + kFlatU * 1024 - 1) / (kFlatU * 1024);
+#if Q27H_PERSIST
+  const size_t grid = blocks < (size_t)Q27H_PERSIST ? blocks : (size_t)Q27H_PERSIST;
+  if (swiglu)
+    hipLaunchKernelGGL(flat_q8_persist_kernel<true>, dim3((unsigned)grid), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n, blocks);
+  else
+    hipLaunchKernelGGL(flat_q8_persist_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n, blocks);
+#else
   if (swiglu)
     hipLaunchKernelGGL(flat_q8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
   else
     hipLaunchKernelGGL(flat_q8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
+#endif
   return check_launch(fn);
 }
 
@@ -262,7 +355,7 @@ extern "C" int q27h_gated_rmsnorm_q8(const float* o, const float* w, const float
   if (!o || !w || !z || !xq || !xd) return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: null pointer");
   if (!aligned16(o) || !aligned16(w) || !aligned16(z) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: o, w, z need 16-byte and xq 4-byte alignment");
-  hipLaunchKernelGGL(gated_rmsnorm_q8_kernel, dim3((heads + 7) / 8), dim3(256), 0, stream_of(s), o, w, z, xq, xd, eps, xs,
+  hipLaunchKernelGGL(gated_rmsnorm_q8_kernel, dim3((heads + 8 * kGatedH - 1) / (8 * kGatedH)), dim3(256), 0, stream_of(s), o, w, z, xq, xd, eps, xs,
                      heads);
   return check_launch("gated_rmsnorm_q8");
 }

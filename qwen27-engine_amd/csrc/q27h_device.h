@@ -2,8 +2,8 @@
 //
 // Numerics contract (identical on the CPU checker): no FP contraction (built with -ffp-contract=off),
 // rsqrt = 1.0f / sqrtf, correctly rounded division and sqrt, exp/log/sin/cos from the routines below.
-// Lane exchanges use DPP (quad permutes, 16-lane row rotate) and ds_swizzle (xor inside 32 lanes); they
-// only move values, so every reduction below adds exactly the operands the reference's 32-lane
+// Lane exchanges use DPP (quad permutes, 16-lane row rotates), v_permlane16_swap (xor 16) and ds_swizzle /
+// ds_bpermute for the remaining patterns; they only move values, so every reduction below adds exactly the operands the reference's 32-lane
 // butterflies add (src/ops.cu:34-50, src/common.cuh:68-87).
 #pragma once
 #include <hip/hip_runtime.h>
@@ -229,6 +229,19 @@ __device__ __forceinline__ float vwarp_sum4(float (&s)[4]) {
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*)p; }
+// 16-byte streaming load (nontemporal hint: the data is read once).
+typedef float q27_v4f __attribute__((ext_vector_type(4)));
+#ifndef Q27H_NT
+#define Q27H_NT 1
+#endif
+__device__ __forceinline__ float4 ld4_nt(const float* p) {
+#if Q27H_NT
+  const q27_v4f v = __builtin_nontemporal_load((const q27_v4f*)p);
+  return make_float4(v.x, v.y, v.z, v.w);
+#else
+  return *(const float4*)p;
+#endif
+}
 __device__ __forceinline__ void st4(float* p, float a, float b, float c, float d) { *(float4*)p = make_float4(a, b, c, d); }
 
 }  // namespace q27h
