@@ -240,18 +240,16 @@ class Pass:
             a[2] += b
 
 
-def cpu_baseline(rows=8):
-    """The CPU oracle (scalar C, one thread) on a bounded sample of the same prefill pass: the 322 launches of
-    one 2048-token batch restricted to `rows` token rows (embedding rows, row-engine rows, GDN tokens, attention
-    tokens), with the byte counts scaled the same way. Returns GB/s and the sample description."""
+def _cpu_pass(M, seed):
+    """The CPU oracle (scalar C) over the 322 launches of one prefill pass restricted to M token rows. Returns the
+    algorithmic bytes it moved (the same per-row definitions as the GPU step)."""
     import numpy as np
 
     sys.path.insert(0, ROOT)
     from oracle import q27_oracle as O
 
-    r = np.random.default_rng(5)
+    r = np.random.default_rng(seed)
     f = lambda n, s=1.0, m=0.0: (r.standard_normal(n) * s + m).astype(np.float32)  # noqa: E731
-    M = rows
     x, part, w = f(M * E), f(M * E), f(E, 0.1, 1.0)
     g, u = f(M * FF, 2.0), f(M * FF, 2.0)
     o, z, w128 = f(M * HV * D), f(M * HV * D), f(D, 0.1, 1.0)
@@ -266,27 +264,195 @@ def cpu_baseline(rows=8):
     table.reshape(-1, 82)[:, 0:2] = np.array([0.01], np.float16).view(np.uint8)
     ids = r.integers(0, 64, M).astype(np.int32)
     ts = float(np.float32(1e7) ** np.float32(-2.0 / 64))
-    total_bytes = 0
-    t0 = time.perf_counter()
+    total = 0
     O.get_rows("iq2_s", table, 1640, ids, E)
-    total_bytes += bytes_get_rows(M, M, 1640)
+    total += bytes_get_rows(M, M, 1640)
     O.rmsnorm_q8(x, w, E, M, EPS, with_h=True, with_xs=True)
-    total_bytes += bytes_rmsnorm_q8(M, True, True)
+    total += bytes_rmsnorm_q8(M, True, True)
     for il in range(N_LAYER):
         if not is_attn(il):
             O.gdn_conv_prefill(qkv, cw, planes, 0, C, M, 2 * KH, EPS, ab[:M * HV], ab[M * HV:], sa, dtb, HV)
             O.gated_rmsnorm_q8(o, w128, z, M * HV, EPS, with_xs=True)
-            total_bytes += bytes_gdn_conv(M) + bytes_gated(M * HV, True)
+            total += bytes_gdn_conv(M) + bytes_gated(M * HV, True)
         else:
             O.attn_prep(qg, k, v, qw, kw, kc, vc, 512, M, EPS, ts, NQH, NKVH, n_ctx, True)
             O.quantize_q8_1(attn_o, NQH * 256, M, with_xs=True)
-            total_bytes += bytes_attn_prep(M) + bytes_quantize(M * NQH * 256, True)
+            total += bytes_attn_prep(M) + bytes_quantize(M * NQH * 256, True)
         O.sum_norm_rows(x, part, w, E, M, EPS)
         O.swiglu_q8(g, u, with_xs=True)
         O.sum_norm_rows(x, part, w, E, M, EPS)
-        total_bytes += 2 * bytes_sum_norm(M, False, True) + bytes_swiglu_q8(M * FF, True)
+        total += 2 * bytes_sum_norm(M, False, True) + bytes_swiglu_q8(M * FF, True)
+    return total
+
+
+def cpu_baseline(rows, threads):
+    """The oracle on a bounded sample of the prefill pass: `rows` token rows split over `threads` host threads (the
+    C calls release the GIL). Returns (GB/s, seconds)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    per = max(1, rows // threads)
+    t0 = time.perf_counter()
+    if threads == 1:
+        total = _cpu_pass(per, 5)
+    else:
+        with ThreadPoolExecutor(threads) as ex:
+            total = sum(ex.map(lambda i: _cpu_pass(per, 5 + i), range(threads)))
     dt = time.perf_counter() - t0
-    return total_bytes / dt / 1e9, dt, f"one prefill pass (64 layers, 322 launches) restricted to {M} token rows"
+    return total / dt / 1e9, dt
+
+
+def time_back_to_back(torch, fn, reps):
+    """Average launch time of `fn(i)` over `reps` back-to-back launches between two HIP events (3 warm-up launches)."""
+    for i in range(3):
+        fn(i)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(reps):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
+def time_graph(torch, fn, n):
+    """Median time per launch of `fn` when n launches are replayed from one HIP graph (decode-sized ops)."""
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(n):
+                fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(20):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b) * 1e3 / n)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def bench_gathers(q27, torch, T=2048, U=4):
+    """248320 x 5120 tables, 2048 Zipf(1.1) ids + 4 uniform ids -> f32 rows. GB/s on compulsory bytes
+    (rows written + distinct table rows read) and on logical bytes (every id's table row counted)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    w = torch.arange(1, VOCAB + 1, dtype=torch.float64, device=dev) ** -1.1
+    cdf = torch.cumsum(w, 0)
+    cdf /= cdf[-1].clone()
+    ranks = torch.clamp(torch.searchsorted(cdf, torch.rand(T, dtype=torch.float64, device=dev, generator=g)), max=VOCAB - 1)
+    perm = torch.randperm(VOCAB, device=dev, generator=g)
+    ids = torch.cat([perm[ranks], torch.randint(0, VOCAB, (U,), device=dev, generator=g)]).to(torch.int32)
+    nid = ids.numel()
+    uniq = int(torch.unique(ids).numel())
+    y = torch.empty(nid * E, device=dev)
+    out = {}
+    for kind, bb, bv, doffs in (("q4_k", 144, 256, (0, 2)), ("q6_k", 210, 256, (208,)), ("q8_0", 34, 32, (0,)),
+                                ("iq2_s", 82, 256, (0,))):
+        nblk = VOCAB * (E // bv)
+        tab = torch.randint(0, 256, (nblk, bb), dtype=torch.uint8, device=dev, generator=g)
+        for off in doffs:
+            d = torch.exp2(torch.rand(nblk, device=dev, generator=g) * 6 - 10).to(torch.float16)
+            tab[:, off:off + 2] = d.view(torch.uint8).view(-1, 2)
+        row_bytes = E // bv * bb
+        fn = getattr(q27.ops, "get_rows_" + kind)
+        us = time_back_to_back(torch, lambda i: fn(tab, row_bytes, ids, nid, y, E), 20)
+        comp = nid * E * 4 + uniq * row_bytes
+        logical = nid * (E * 4 + row_bytes)
+        out[kind] = {"us": round(us, 2), "GBps_compulsory": round(comp / us / 1e3, 1),
+                     "GBps_logical": round(logical / us / 1e3, 1), "distinct_ids": uniq, "ids": nid}
+        log(f"  gather {kind:6s} {us:7.2f} us  {comp / us / 1e3:7.1f} GB/s compulsory  {logical / us / 1e3:7.1f} GB/s logical")
+        del tab
+    return out
+
+
+def bench_multimodal(q27, torch, M=4099):
+    """4099 rows (3 text + a 64 x 64 image grid): gated_rmsnorm_q8 over 48 value heads, l2norm_heads of
+    the 32 q/k heads (row stride 10240, in place), attn_prep with IMRoPE positions (t, h, w)."""
+    dev = torch.device("cuda:0")
+    rn = lambda n: torch.randn(n, device=dev)  # noqa: E731
+    sets = 3
+    o = [rn(M * HV * D) for _ in range(sets)]
+    z = [rn(M * HV * D) for _ in range(sets)]
+    w128 = rn(D) * 0.1 + 1
+    xq = torch.empty(M * HV * D, dtype=torch.int8, device=dev)
+    xd = torch.empty(M * HV * D // 32, device=dev)
+    xs = torch.empty(M * HV * D // 16, device=dev)
+    res = {}
+    us = time_back_to_back(torch, lambda i: q27.ops.gated_rmsnorm_q8(o[i % sets], w128, z[i % sets], xq, xd, M * HV, EPS, None, xs), 21)
+    b = bytes_gated(M * HV, True)
+    res["gated_rmsnorm_q8"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "bytes": b}
+    del o, z
+    conv = [rn(M * C) for _ in range(sets)]
+    us = time_back_to_back(torch, lambda i: q27.ops.l2norm_heads(conv[i % sets], D, 2 * KH, M, C, EPS), 21)
+    b = M * 2 * KH * D * 8
+    res["l2norm_heads"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "bytes": b}
+    del conv
+    rows = [(p, p, p) for p in range(3)] + [(3, 3 + i // 64, 3 + i % 64) for i in range(4096)]
+    rope3 = torch.tensor(rows, dtype=torch.int32, device=dev).reshape(-1)
+    qg = [rn(M * NQH * 512) for _ in range(sets)]
+    k, v = rn(M * NKVH * 256), rn(M * NKVH * 256)
+    qn = torch.empty(M * NQH * 256, device=dev)
+    n_ctx = 8192
+    cb = q27.ops.kv_cache_bytes(NKVH, n_ctx, True)
+    kc, vc = torch.zeros(cb, dtype=torch.uint8, device=dev), torch.zeros(cb, dtype=torch.uint8, device=dev)
+    pos0 = torch.zeros(1, dtype=torch.int32, device=dev)
+    ts = float(torch.tensor(1e7) ** torch.tensor(-2.0 / 64))
+    us = time_back_to_back(torch, lambda i: q27.ops.attn_prep(qg[i % sets], k, v, w128.repeat(2), w128.repeat(2), qn, kc, vc,
+                                                                pos0, M, EPS, ts, NQH, NKVH, n_ctx, True, None, None, 0,
+                                                                rope3, None), 21)
+    b = bytes_attn_prep(M)
+    res["attn_prep_imrope"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "bytes": b}
+    for k_, v_ in res.items():
+        log(f"  cfg5 {k_:18s} {v_['us']:7.2f} us  {v_['GBps']:7.1f} GB/s")
+    return res
+
+
+def bench_cfg1(q27, torch):
+    """RMSNorm -> q8_1 of one 5120 row (0.1% outliers x50) on the CPU oracle and on the GPU, with the
+    bit-exact comparison of xq / xd / xs."""
+    import numpy as np
+
+    sys.path.insert(0, ROOT)
+    from oracle import q27_oracle as O
+
+    r = np.random.default_rng(1)
+    x = r.standard_normal(E).astype(np.float32)
+    x[r.choice(E, 5, replace=False)] *= 50
+    w = (r.standard_normal(E) * 0.1 + 1).astype(np.float32)
+    t0 = time.perf_counter()
+    for _ in range(200):
+        _, oq, od, os_ = O.rmsnorm_q8(x, w, E, 1, EPS, with_h=False, with_xs=True)
+    cpu_us = (time.perf_counter() - t0) / 200 * 1e6
+    dx, dw = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    xq = torch.empty(E, dtype=torch.int8, device="cuda")
+    xd, xs = torch.empty(E // 32, device="cuda"), torch.empty(E // 16, device="cuda")
+    fn = lambda: q27.ops.rmsnorm_q8(dx, dw, None, xq, xd, E, 1, EPS, None, xs)  # noqa: E731
+    gpu_us = time_graph(torch, fn, 50)
+    exact = (np.array_equal(xq.cpu().numpy(), oq) and np.array_equal(xd.cpu().numpy().view(np.uint32), od.view(np.uint32))
+             and np.array_equal(xs.cpu().numpy().view(np.uint32), os_.view(np.uint32)))
+    log(f"  cfg1 rmsnorm_q8 1x5120: cpu oracle {cpu_us:.1f} us (1 thread), gpu {gpu_us:.2f} us, bit-exact {exact}")
+    return {"cpu_us_1thread": round(cpu_us, 2), "gpu_us_graph": round(gpu_us, 2), "bytes": 48000, "bit_exact": bool(exact)}
+
+
+def bench_decode_ops(q27, torch, Dp):
+    """configs[1] per op: median time per launch with 50 launches of the op replayed from one HIP graph."""
+    res = {}
+    seen = set()
+    for name, b, fn in Dp.launches:
+        if name in seen:
+            continue
+        seen.add(name)
+        us = time_graph(torch, fn, 50)
+        res[name] = {"us": round(us, 2), "bytes": b}
+        log(f"  decode {name:18s} {us:6.2f} us per launch (graph)")
+    return res
 
 
 def main():
@@ -296,7 +462,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--graph-replays", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
-    ap.add_argument("--cpu-rows", type=int, default=128)
+    ap.add_argument("--cpu-rows", type=int, default=256)
     ap.add_argument("--calib-copy", action="store_true", help="also run a plain 256 MiB copy (rocprof counter calibration)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
@@ -416,7 +582,16 @@ def main():
     times.sort()
     decode_us = times[len(times) // 2]
     log(f"decode verify pass: {len(Dp.launches)} launches in one graph, median {decode_us:.1f} us")
-    del graph, Dp
+    del graph
+    decode_ops = bench_decode_ops(q27, torch, Dp)
+    del Dp
+    torch.cuda.empty_cache()
+
+    # ---- configs[0], configs[3] (gathers) and configs[4] (multimodal + GDN)
+    cfg1 = bench_cfg1(q27, torch)
+    gathers = bench_gathers(q27, torch)
+    torch.cuda.empty_cache()
+    multimodal = bench_multimodal(q27, torch)
     torch.cuda.empty_cache()
 
     if args.calib_copy:
@@ -429,10 +604,16 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        gbs, secs, sample = cpu_baseline(args.cpu_rows)
-        cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{sample}; {secs:.1f} s on the host", "us_per_2048_batch_equiv": round(step_bytes / (gbs * 1e9) * 1e6, 0)}
-        log(f"cpu oracle: {gbs:.3f} GB/s ({secs:.1f} s)")
+        threads = min(16, os.cpu_count() or 1)
+        gbs1, secs1 = cpu_baseline(args.cpu_rows // 4, 1)
+        gbsn, secsn = cpu_baseline(args.cpu_rows, threads)
+        cpu = {"value": round(gbsn, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": (f"the prefill pass (64 layers, 322 launches of the oracle) on {args.cpu_rows} token rows split over "
+                          f"{threads} threads: {secsn:.1f} s; single thread on {args.cpu_rows // 4} rows: {gbs1:.3f} GB/s "
+                          f"({secs1:.1f} s)"),
+               "single_thread_GBps": round(gbs1, 3),
+               "us_per_2048_batch_equiv": round(step_bytes / (gbsn * 1e9) * 1e6, 0)}
+        log(f"cpu oracle: {gbsn:.3f} GB/s on {threads} threads ({secsn:.1f} s), {gbs1:.3f} GB/s on 1 thread ({secs1:.1f} s)")
 
     out = {
         "metric": "achieved HBM GB/s of the fused per-layer ops over one 2048-token prefill pass",
@@ -447,6 +628,10 @@ def main():
         "us_per_2048_batch": round(ms_per_step * 1e3, 1),
         "decode_us_per_step": round(decode_us, 1),
         "per_op": per_op,
+        "decode_per_op": decode_ops,
+        "cfg1_rmsnorm_q8_row": cfg1,
+        "gathers_cfg4": gathers,
+        "multimodal_cfg5": multimodal,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -2,17 +2,14 @@
 // (gdn_conv_l2, T <= 4 with state snapshots) and prefill (gdn_conv_prefill, M tokens, state plane flip), plus the
 // unfused twins gdn_conv / gdn_gates / l2norm_heads.
 //
-// Fused layout: 32 lanes (half a wave) per (head of 128 channels, chunk of tokens); lane p owns channels
-// 4p .. 4p+3, so every token row of a head is one 512-byte load and store, and the conv window of the last three
-// inputs stays in registers while the lanes walk the chunk's tokens. The L2 norm reproduces the reference's
+// Fused layout: 32 lanes (half a wave) per (head of 128 channels, token or chunk of tokens); lane p owns channels
+// 4p .. 4p+3, so every token row of a head is one 512-byte load and store, and in prefill the conv window of the
+// last three inputs stays in registers while the lanes walk the chunk's tokens. The L2 norm reproduces the reference's
 // warp-per-head order (src/ops.cu:318-330, 442-446): virtual lane v sums y[v]^2, y[v+32]^2, y[v+64]^2, y[v+96]^2
 // in that order, then the xor butterfly; those four values sit in lanes (p & 7) + 8k, fetched with ds_swizzle.
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
-#ifndef Q27H_GDN_PRELOAD
-#define Q27H_GDN_PRELOAD 0
-#endif
 #ifndef Q27H_GDN_CH
 #define Q27H_GDN_CH 16
 #endif
@@ -57,28 +54,28 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
   g[i] = q27_softplus(a[i] + dt_bias[hv]) * ssm_a[hv];
 }
 
-template <bool PREFILL, int CH>
-__global__ void __launch_bounds__(256) gdn_conv_fused_kernel(const float* __restrict__ x, const float* __restrict__ cw,
-                                                             float* __restrict__ planes, const int* __restrict__ in_plane,
-                                                             float* __restrict__ y, int C, int T, int snapshots,
-                                                             int n_norm_heads, float eps, const float* __restrict__ a,
-                                                             const float* __restrict__ b, const float* __restrict__ ssm_a,
-                                                             const float* __restrict__ dt_bias, float* __restrict__ g,
-                                                             float* __restrict__ beta, int H, int nchunks) {
+// Prefill: 32 lanes per (head of 128 channels, chunk of CH tokens), a workgroup = 8 neighbouring heads of one
+// chunk. The conv window of a chunk starts with the 3 rows before it, which the previous chunk of the same heads
+// has just read: workgroups are numbered so that each XCD (workgroup id mod 8) walks a contiguous range of
+// (head group, chunk) tiles in chunk order, and those rows are L2 hits instead of HBM re-reads.
+template <int CH>
+__global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __restrict__ x, const float* __restrict__ cw,
+                                                               float* __restrict__ planes, const int* __restrict__ in_plane,
+                                                               float* __restrict__ y, int C, int T, int n_norm_heads,
+                                                               float eps, const float* __restrict__ a,
+                                                               const float* __restrict__ b, const float* __restrict__ ssm_a,
+                                                               const float* __restrict__ dt_bias, float* __restrict__ g,
+                                                               float* __restrict__ beta, int H, int nchunks, int tiles_per_xcd) {
   const int nheads = C / 128;
-  const int item = blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (item >= nheads * nchunks) return;  // whole halves leave together
-  const int head = item % nheads, ch = item / nheads;  // neighbouring halves: neighbouring heads of one token range
+  const int ngroups = (nheads + 7) / 8;
+  const int tile = (blockIdx.x & 7) * tiles_per_xcd + (blockIdx.x >> 3);  // XCD-major order of the tiles
+  if (tile >= ngroups * nchunks) return;
+  const int group = tile / nchunks, ch = tile % nchunks;
+  const int head = group * 8 + (threadIdx.x >> 5);
+  if (head >= nheads) return;  // whole halves leave together
   const int p = threadIdx.x & 31;
   const int c0 = head * 128 + 4 * p;
   const int t0 = ch * CH, t1 = min(T, t0 + CH);
-#if Q27H_GDN_PRELOAD
-  // every input row of the chunk is loaded before the first token is processed
-  float4 xr[CH];
-#pragma unroll
-  for (int i = 0; i < CH; i++)
-    if (t0 + i < t1) xr[i] = ld4(x + (size_t)(t0 + i) * C + c0);
-#endif
   const int pin = *in_plane;
   float w[4][4];
 #pragma unroll
@@ -88,42 +85,31 @@ __global__ void __launch_bounds__(256) gdn_conv_fused_kernel(const float* __rest
   }
   // conv window: s0, s1, s2 = inputs t0-3, t0-2, t0-1 (state plane `pin` before the batch)
   float s0[4], s1[4], s2[4];
-  {
+  if (t0 == 0) {
     const float* st = planes + ((size_t)pin * C + c0) * 3;  // 12 floats: channel c taps at 3c .. 3c+2
     const float4 q0 = ld4(st), q1 = ld4(st + 4), q2 = ld4(st + 8);
     const float sv[12] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w};
 #pragma unroll
     for (int c = 0; c < 4; c++) { s0[c] = sv[3 * c]; s1[c] = sv[3 * c + 1]; s2[c] = sv[3 * c + 2]; }
-    if (PREFILL && t0 > 0) {
-      const float4 r0 = ld4(x + (size_t)(t0 - 3) * C + c0), r1 = ld4(x + (size_t)(t0 - 2) * C + c0),
-                   r2 = ld4(x + (size_t)(t0 - 1) * C + c0);
-      s0[0] = r0.x; s0[1] = r0.y; s0[2] = r0.z; s0[3] = r0.w;
-      s1[0] = r1.x; s1[1] = r1.y; s1[2] = r1.z; s1[3] = r1.w;
-      s2[0] = r2.x; s2[1] = r2.y; s2[2] = r2.z; s2[3] = r2.w;
-    }
+  } else {
+    const float4 r0 = ld4(x + (size_t)(t0 - 3) * C + c0), r1 = ld4(x + (size_t)(t0 - 2) * C + c0),
+                 r2 = ld4(x + (size_t)(t0 - 1) * C + c0);
+    s0[0] = r0.x; s0[1] = r0.y; s0[2] = r0.z; s0[3] = r0.w;
+    s1[0] = r1.x; s1[1] = r1.y; s1[2] = r1.z; s1[3] = r1.w;
+    s2[0] = r2.x; s2[1] = r2.y; s2[2] = r2.z; s2[3] = r2.w;
   }
   const bool norm = head < n_norm_heads;
 #pragma unroll
   for (int i = 0; i < CH; i++) {
     const int t = t0 + i;
     if (t >= t1) break;
-#if Q27H_GDN_PRELOAD
-    const float xn[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-#else
     const float4 xv = ld4(x + (size_t)t * C + c0);
     const float xn[4] = {xv.x, xv.y, xv.z, xv.w};
-#endif
     float out[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       out[c] = q27_silu(conv4(s0[c], s1[c], s2[c], xn[c], w[c]));
       s0[c] = s1[c]; s1[c] = s2[c]; s2[c] = xn[c];
-    }
-    if (!PREFILL && (snapshots || t == T - 1)) {
-      float* o = planes + ((size_t)t * C + c0) * 3;
-      st4(o, s0[0], s1[0], s2[0], s0[1]);
-      st4(o + 4, s1[1], s2[1], s0[2], s1[2]);
-      st4(o + 8, s2[2], s0[3], s1[3], s2[3]);
     }
     if (norm) l2_head_lanes(out, eps);
     st4(y + (size_t)t * C + c0, out[0], out[1], out[2], out[3]);
@@ -132,12 +118,77 @@ __global__ void __launch_bounds__(256) gdn_conv_fused_kernel(const float* __rest
     const int hv = head - n_norm_heads;
     for (int t = t0 + p; t < t1; t += 32) gate_one(a, b, ssm_a, dt_bias, g, beta, t, H, hv);
   }
-  if (PREFILL && t1 == T) {  // state after the batch: inputs T-3 .. T-1 (from the old state when T < 3)
+  if (t1 == T) {  // state after the batch: inputs T-3 .. T-1 (from the old state when T < 3)
     float* o = planes + ((size_t)(pin == 0 ? 1 : 0) * C + c0) * 3;
     st4(o, s0[0], s1[0], s2[0], s0[1]);
     st4(o + 4, s1[1], s2[1], s0[2], s1[2]);
     st4(o + 8, s2[2], s0[3], s1[3], s2[3]);
   }
+}
+
+// Decode (T <= 4, src/ops.cu:288-338): one 128-thread workgroup per head, 32 lanes per token, so the T tokens run
+// side by side. Token t's window is inputs t-3 .. t-1 (the state plane `pin` for negative ones); snapshot plane t
+// receives inputs t-2 .. t. Planes are read before the barrier and written after it, because a snapshot may
+// overwrite plane `pin` while another token still needs it.
+__global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __restrict__ x, const float* __restrict__ cw,
+                                                              float* __restrict__ planes, const int* __restrict__ in_plane,
+                                                              float* __restrict__ y, int C, int T, int snapshots,
+                                                              int n_norm_heads, float eps, const float* __restrict__ a,
+                                                              const float* __restrict__ b, const float* __restrict__ ssm_a,
+                                                              const float* __restrict__ dt_bias, float* __restrict__ g,
+                                                              float* __restrict__ beta, int H) {
+  const int head = blockIdx.x;
+  const int t = threadIdx.x >> 5, p = threadIdx.x & 31;
+  const int c0 = head * 128 + 4 * p;
+  const bool active = t < T;
+  const int pin = *in_plane;
+  float in[7][4];  // inputs -3 .. 3 of the lane's 4 channels; token t uses in[t .. t+3]
+  {
+    const float* st = planes + ((size_t)pin * C + c0) * 3;
+    const float4 q0 = ld4(st), q1 = ld4(st + 4), q2 = ld4(st + 8);
+    const float sv[12] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) { in[0][c] = sv[3 * c]; in[1][c] = sv[3 * c + 1]; in[2][c] = sv[3 * c + 2]; }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    if (r < T && r <= t) {
+      const float4 xv = ld4(x + (size_t)r * C + c0);
+      in[3 + r][0] = xv.x; in[3 + r][1] = xv.y; in[3 + r][2] = xv.z; in[3 + r][3] = xv.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++) in[3 + r][c] = 0.0f;
+    }
+  }
+  float w[4][4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float4 wv = ld4(cw + 4 * (size_t)(c0 + c));
+    w[c][0] = wv.x; w[c][1] = wv.y; w[c][2] = wv.z; w[c][3] = wv.w;
+  }
+  // window of token t (registers, selected with constant indices)
+  float s0[4], s1[4], s2[4], xn[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    s0[c] = t == 0 ? in[0][c] : t == 1 ? in[1][c] : t == 2 ? in[2][c] : in[3][c];
+    s1[c] = t == 0 ? in[1][c] : t == 1 ? in[2][c] : t == 2 ? in[3][c] : in[4][c];
+    s2[c] = t == 0 ? in[2][c] : t == 1 ? in[3][c] : t == 2 ? in[4][c] : in[5][c];
+    xn[c] = t == 0 ? in[3][c] : t == 1 ? in[4][c] : t == 2 ? in[5][c] : in[6][c];
+  }
+  __syncthreads();  // every plane read of the workgroup is consumed before any snapshot write
+  if (!active) return;
+  float out[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) out[c] = q27_silu(conv4(s0[c], s1[c], s2[c], xn[c], w[c]));
+  if (snapshots || t == T - 1) {
+    float* o = planes + ((size_t)t * C + c0) * 3;
+    st4(o, s1[0], s2[0], xn[0], s1[1]);
+    st4(o + 4, s2[1], xn[1], s1[2], s2[2]);
+    st4(o + 8, xn[2], s1[3], s2[3], xn[3]);
+  }
+  if (head < n_norm_heads) l2_head_lanes(out, eps);
+  else if (p == 0) gate_one(a, b, ssm_a, dt_bias, g, beta, t, H, head - n_norm_heads);
+  st4(y + (size_t)t * C + c0, out[0], out[1], out[2], out[3]);
 }
 
 // l2norm_heads for n = 128: 8 lanes per (token, head); lane q loads channels 4q + 32k (k = 0..3), i.e. the
@@ -240,9 +291,8 @@ extern "C" int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, c
     return e;
   if (T > 4) return fail(Q27H_ERR_SHAPE, "gdn_conv_l2: T must be <= 4 (4 state planes)");
   if (T == 0) return Q27H_OK;
-  const int items = C / 128;
-  hipLaunchKernelGGL((gdn_conv_fused_kernel<false, 4>), dim3((items + 7) / 8), dim3(256), 0, stream_of(s), x, w, planes,
-                     in_plane, y, C, T, snapshots, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, 1);
+  hipLaunchKernelGGL(gdn_conv_decode_kernel, dim3(C / 128), dim3(128), 0, stream_of(s), x, w, planes, in_plane, y, C, T,
+                     snapshots, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H);
   return check_launch("gdn_conv_l2");
 }
 
@@ -254,9 +304,10 @@ extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* plan
   if (M == 0) return Q27H_OK;
   constexpr int chunk = Q27H_GDN_CH;  // tokens per half-wave; >= 3 so a chunk's window never reaches past the previous chunk
   const int nchunks = (M + chunk - 1) / chunk;
-  const long items = (long)(C / 128) * nchunks;
-  hipLaunchKernelGGL((gdn_conv_fused_kernel<true, chunk>), dim3((unsigned)((items + 7) / 8)), dim3(256), 0, stream_of(s), x, w,
-                     planes, in_plane, y, C, M, 0, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, nchunks);
+  const long tiles = (long)((C / 128 + 7) / 8) * nchunks;
+  const int tiles_per_xcd = (int)((tiles + 7) / 8);
+  hipLaunchKernelGGL((gdn_conv_prefill_kernel<chunk>), dim3((unsigned)(8 * tiles_per_xcd)), dim3(256), 0, stream_of(s), x, w,
+                     planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, nchunks, tiles_per_xcd);
   return check_launch("gdn_conv_prefill");
 }
 

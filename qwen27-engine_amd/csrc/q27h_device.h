@@ -79,11 +79,11 @@ __device__ __forceinline__ float bf16_to_f(uint16_t b) { return __builtin_bit_ca
 // exp: Cody-Waite reduction x = k ln2 + r, degree-7 Taylor polynomial of e^r (Horner, fma), ldexp.
 // Same operations and constants as the CPU checker (Muller, Elementary Functions, ch. 11).
 __device__ __forceinline__ float q27_expf(float x) {
-  if (x != x) return x + x;
-  if (x > 88.7228394f) return __builtin_huge_valf();
-  if (x < -103.972084f) return 0.0f;
-  const float k = __builtin_rintf(x * 1.44269502f);
-  float r = __builtin_fmaf(-k, 0.693145752f, x);
+  // Branch-free: the polynomial is evaluated on a clamped argument and the out-of-range results are selected
+  // afterwards, giving the same values as the early-return form of the CPU checker.
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -103.972084f), 88.7228394f);
+  const float k = __builtin_rintf(xc * 1.44269502f);
+  float r = __builtin_fmaf(-k, 0.693145752f, xc);
   r = __builtin_fmaf(-k, 1.42860677e-06f, r);
   float p = 1.98412698e-4f;
   p = __builtin_fmaf(p, r, 1.38888889e-3f);
@@ -93,7 +93,10 @@ __device__ __forceinline__ float q27_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  return __builtin_ldexpf(p, (int)k);
+  float e = __builtin_ldexpf(p, (int)k);
+  e = x > 88.7228394f ? __builtin_huge_valf() : e;
+  e = x < -103.972084f ? 0.0f : e;
+  return x != x ? x + x : e;
 }
 
 // log for the softplus gate: x = 2^e m, m in [sqrt(1/2), sqrt(2)), s = f / (2 + f), log m = 2 atanh(s) as an
@@ -167,15 +170,25 @@ __device__ __forceinline__ void q27_sincos(float theta, float* s_out, float* c_o
 }
 
 // ---------------------------------------------------------------- q8 rounding
-// roundf(y / d) for |y| <= 127 d, d > 0 (the q8_1 rule of src/common.cuh:76). y * (1/d) is within 2.3e-5 of the
-// correctly rounded quotient, so away from the half-integers it rounds the same way and rintf == roundf; within
-// 2^-12 of a half-integer (or for non-finite 1/d) the IEEE quotient is taken.
-__device__ __forceinline__ int q8_round_div(float y, float d, float rd) {
-  const float a = y * rd;
-  const float fa = __builtin_fabsf(a);
-  const float fr = fa - __builtin_floorf(fa);
-  if (__builtin_fabsf(fr - 0.5f) > 2.44140625e-4f) return (int)__builtin_rintf(a);
-  return (int)__builtin_roundf(y / d);
+// roundf(y / d) for |y| <= 127 d, d > 0 (the q8_1 rule of src/common.cuh:76), four values at a time. y * (1/d) is
+// within 2.3e-5 of the correctly rounded quotient, so away from the half-integers it rounds the same way and
+// rintf == roundf; a value within 2^-12 of a half-integer (or any value when 1/d is not finite) takes the IEEE
+// quotient. The rare exact path is one branch per four values.
+__device__ __forceinline__ void q8_round_div4(const float (&y)[4], float d, int (&q)[4]) {
+  const float rd = 1.0f / d;
+  bool slow = false;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float a = y[c] * rd;
+    const float fa = __builtin_fabsf(a);
+    const float fr = fa - __builtin_floorf(fa);
+    slow |= !(__builtin_fabsf(fr - 0.5f) > 2.44140625e-4f);
+    q[c] = (int)__builtin_rintf(a);
+  }
+  if (slow) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) q[c] = (int)__builtin_roundf(y[c] / d);
+  }
 }
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
@@ -196,11 +209,7 @@ __device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restr
   amax = __builtin_fmaxf(amax, lane_xor<1>(amax));
   const float d = amax / 127.0f;
   int q[4] = {0, 0, 0, 0};
-  if (amax != 0.0f) {
-    const float rd = 1.0f / d;
-#pragma unroll
-    for (int c = 0; c < 4; c++) q[c] = q8_round_div(y[c], d, rd);
-  }
+  if (amax != 0.0f) q8_round_div4(y, d, q);
   *(uint32_t*)(xq + i0) = pack4_i8(q[0], q[1], q[2], q[3]);
   const int sub = (int)((i0 >> 2) & 7);
   if (sub == 0) xd[i0 >> 5] = fp16_round(d);

@@ -129,6 +129,26 @@ def test_quantize_q8_1(q27, oracle, T, ncols, K):
         assert_bits_equal(T.down(got), want, what)
 
 
+def test_q8_rounding_near_half_integers(q27, oracle, T):
+    """Values whose quotient y / d lies on or within a few ulps of k + 0.5: the fast y * (1/d) path must hand these to
+    the IEEE quotient (roundf, ties away from zero), exactly as the oracle rounds them."""
+    say("q8_1 rounding near half-integers")
+    r = cd.rng(123)
+    nblk = 4096
+    amax = np.exp(r.uniform(-8, 8, nblk)).astype(np.float32)
+    d = amax / np.float32(127)
+    k = r.integers(-126, 126, (nblk, 31)).astype(np.float32)
+    y = ((k + np.float32(0.5)) * d[:, None]).astype(np.float32)
+    ulps = r.integers(-3, 4, (nblk, 31)).astype(np.int32)
+    y = (y.view(np.int32) + ulps).view(np.float32)  # on the tie and a few ulps either side
+    x = np.concatenate([amax[:, None], y], 1).reshape(-1)  # lane 0 of each block fixes amax (and so d)
+    xq, xd, xs = q8_bufs(T, x.size, True)
+    q27.ops.quantize_q8_1(T.up(x), xq, xd, x.size, 1, None, xs)
+    oq, od, os_ = oracle.quantize_q8_1(x, x.size, 1, with_xs=True)
+    for got, want, what in ((xq, oq, "xq"), (xd, od, "xd"), (xs, os_, "xs")):
+        assert_bits_equal(T.down(got), want, what)
+
+
 @pytest.mark.parametrize("n,with_xs", [(4 * FF, False), (2048 * FF, True), (96, True)])
 def test_swiglu_q8(q27, oracle, T, n, with_xs):
     say(f"swiglu_q8 n={n}")
