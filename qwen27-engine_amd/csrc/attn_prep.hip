@@ -1,11 +1,11 @@
 // Attention input stage (attn_prep): per-head RMSNorm of q and k, partial NeoX rotary (plain positions or
 // IMRoPE sections), and the K/V cache write as f16 or q8_0.
 //
-// Lane p of a wave holds head dims 4p .. 4p+3 (16-byte loads and stores). The reference's
+// Lane p of a wave holds 4 head dims in the 32-value block layout of q27h_device.h (16-byte loads and stores). The reference's
 // 256-thread block_sum (src/ops.cu:609) is rebuilt from the same operands: per virtual warp of 32 dims
 // (8 lanes) vwarp_sum4, then the second stage over the 8 warp sums w_g (lanes 8g..8g+7), whose reference tree
 // ((w0+w4)+(w2+w6)) + ((w1+w5)+(w3+w7)) is lane xor 32, xor 16, xor 8. The rotary partner of dim j < 32 is dim
-// j + 32, i.e. lane p ^ 8 (a DPP row rotate). Angles are (float)p * freq[j] with freq[j] = theta_scale^j taken
+// j + 32, i.e. the same lane of the next 8-lane group, lane p ^ 8 (a DPP row rotate). Angles are (float)p * freq[j] with freq[j] = theta_scale^j taken
 // once on the host; sin and cos come from the shared double-precision routine.
 #include <cmath>
 
@@ -24,6 +24,10 @@ struct RopeFreqs {
 // HPW = 1 for a few tokens, where the shorter chain per wave matters more than loads in flight. The 32 rotary angles of the token are evaluated
 // once per wave (lane j < 32 takes pair j) and handed to the lanes that need them with ds_bpermute; the head
 // vectors of the whole group are loaded before any arithmetic.
+#ifndef Q27H_ATTN_HPW
+#define Q27H_ATTN_HPW 4
+#endif
+
 template <int HPW>
 __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict__ qg, const float* __restrict__ k,
                                                         const float* __restrict__ v, const float* __restrict__ q_norm,
@@ -40,6 +44,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
   const int hb0 = (wave % wpt) * HPW;
   const int nhw = min(HPW, nh - hb0);
   const int p = threadIdx.x & 63;
+  const int off = 32 * (p >> 3) + block_offset(p);  // this lane's 4 head dims (32-value block layout)
   const int pos = *dpos0 + tok;  // cache row
   // ---- loads of the whole group
   float4 xin[HPW], vin[HPW];
@@ -48,16 +53,16 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
     const int hb = hb0 + i;
     if (i < nhw) {
       if (hb < nqh) {
-        xin[i] = ld4(qg + ((size_t)tok * nqh + hb) * 512 + 4 * p);
+        xin[i] = ld4(qg + ((size_t)tok * nqh + hb) * 512 + off);
       } else {
-        const size_t off = ((size_t)tok * nkvh + (hb - nqh)) * 256 + 4 * p;
-        xin[i] = ld4(k + off);
-        vin[i] = ld4(v + off);
+        const size_t o = ((size_t)tok * nkvh + (hb - nqh)) * 256 + off;
+        xin[i] = ld4(k + o);
+        vin[i] = ld4(v + o);
       }
     }
   }
-  const float4 qw = ld4(q_norm + 4 * p);
-  const float4 kw = nkvh ? ld4(k_norm + 4 * p) : qw;
+  const float4 qw = ld4(q_norm + off);
+  const float4 kw = nkvh ? ld4(k_norm + off) : qw;
   // ---- rotary angles of the token: lane j < 32 evaluates pair j
   float sn_j = 0.0f, cs_j = 1.0f;
   if (p < 32) {
@@ -67,7 +72,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
   float snc[4], csc[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    const int j = (4 * p + c) & 31;
+    const int j = (off + c) & 31;
     snc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, sn_j)));
     csc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, cs_j)));
   }
@@ -108,7 +113,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
       for (int c = 0; c < 4; c++) out[c] = partner[c] * snc[c] + buf[c] * csc[c];   // x0 * s + x1 * c
     }
     if (isq) {
-      st4(qn + ((size_t)tok * nqh + hb) * 256 + 4 * p, out[0], out[1], out[2], out[3]);
+      st4(qn + ((size_t)tok * nqh + hb) * 256 + off, out[0], out[1], out[2], out[3]);
       continue;
     }
     const int kh = hb - nqh;
@@ -116,8 +121,8 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
     const size_t row = (size_t)kh * n_ctx + (size_t)(valid ? pos : 0);
     if (!q8) {
       if (!valid) continue;
-      uint16_t* kc = (uint16_t*)kcache + row * 256 + 4 * p;
-      uint16_t* vc = (uint16_t*)vcache + row * 256 + 4 * p;
+      uint16_t* kc = (uint16_t*)kcache + row * 256 + off;
+      uint16_t* vc = (uint16_t*)vcache + row * 256 + off;
       *(uint2*)kc = make_uint2((uint32_t)f2h_bits(out[0]) | ((uint32_t)f2h_bits(out[1]) << 16),
                                (uint32_t)f2h_bits(out[2]) | ((uint32_t)f2h_bits(out[3]) << 16));
       *(uint2*)vc = make_uint2((uint32_t)f2h_bits(vv[0]) | ((uint32_t)f2h_bits(vv[1]) << 16),
@@ -129,8 +134,8 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
                                __builtin_fmaxf(__builtin_fabsf(out[2]), __builtin_fabsf(out[3])));
     float av = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(vv[0]), __builtin_fabsf(vv[1])),
                                __builtin_fmaxf(__builtin_fabsf(vv[2]), __builtin_fabsf(vv[3])));
-    ak = __builtin_fmaxf(ak, lane_xor<4>(ak));
-    av = __builtin_fmaxf(av, lane_xor<4>(av));
+    ak = __builtin_fmaxf(ak, lane_xor<7>(ak));
+    av = __builtin_fmaxf(av, lane_xor<7>(av));
     ak = __builtin_fmaxf(ak, lane_xor<2>(ak));
     av = __builtin_fmaxf(av, lane_xor<2>(av));
     ak = __builtin_fmaxf(ak, lane_xor<1>(ak));
@@ -138,8 +143,8 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
     if (!valid) continue;
     const float dk = ak / 127.f, dv = av / 127.f;
     const float ik = dk != 0.0f ? 1.0f / dk : 0.0f, iv = dv != 0.0f ? 1.0f / dv : 0.0f;
-    int8_t* kq = (int8_t*)kcache + row * 256 + 4 * p;
-    int8_t* vq = (int8_t*)vcache + row * 256 + 4 * p;
+    int8_t* kq = (int8_t*)kcache + row * 256 + off;
+    int8_t* vq = (int8_t*)vcache + row * 256 + off;
     *(uint32_t*)kq = pack4_i8((int)__builtin_roundf(out[0] * ik), (int)__builtin_roundf(out[1] * ik),
                               (int)__builtin_roundf(out[2] * ik), (int)__builtin_roundf(out[3] * ik));
     *(uint32_t*)vq = pack4_i8((int)__builtin_roundf(vv[0] * iv), (int)__builtin_roundf(vv[1] * iv),
@@ -181,8 +186,9 @@ extern "C" int q27h_attn_prep(const float* qg, const float* k, const float* v, c
     hipLaunchKernelGGL(attn_prep_kernel<1>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm,
                        k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
   } else {
-    const long waves = (long)T * ((nh + 3) / 4);
-    hipLaunchKernelGGL(attn_prep_kernel<4>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm,
+    constexpr int hpw = Q27H_ATTN_HPW;
+    const long waves = (long)T * ((nh + hpw - 1) / hpw);
+    hipLaunchKernelGGL(attn_prep_kernel<hpw>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm,
                        k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
   }
   return check_launch("attn_prep");

@@ -2,8 +2,8 @@
 // (gdn_conv_l2, T <= 4 with state snapshots) and prefill (gdn_conv_prefill, M tokens, state plane flip), plus the
 // unfused twins gdn_conv / gdn_gates / l2norm_heads.
 //
-// Fused layout: 32 lanes (half a wave) per (head of 128 channels, token or chunk of tokens); lane p owns channels
-// 4p .. 4p+3, so every token row of a head is one 512-byte load and store, and in prefill the conv window of the
+// Fused layout: 32 lanes (half a wave) per (head of 128 channels, token or chunk of tokens); lane p owns 4
+// consecutive channels (the 32-value block layout of q27h_device.h), so every token row of a head is one 512-byte load and store, and in prefill the conv window of the
 // last three inputs stays in registers while the lanes walk the chunk's tokens. The L2 norm reproduces the reference's
 // warp-per-head order (src/ops.cu:318-330, 442-446): virtual lane v sums y[v]^2, y[v+32]^2, y[v+64]^2, y[v+96]^2
 // in that order, then the xor butterfly; those four values sit in lanes (p & 7) + 8k, fetched with ds_swizzle.
@@ -26,7 +26,9 @@ __device__ __forceinline__ float conv4(float s0, float s1, float s2, float xn, c
   return sum;
 }
 
-// L2 norm of one 128-channel head held by a 32-lane half, lane p holding channels 4p + c.
+// L2 norm of one 128-channel head held by a 32-lane half in the 32-value block layout (lane p holds channels
+// 32 (p / 8) + 4 quad_of_lane(p % 8) + c): the reference lane v's values v, v + 32, v + 64, v + 96 sit in lanes
+// (p & 7) + 8k, gathered in that order, then the virtual warp butterfly.
 __device__ __forceinline__ void l2_head_lanes(float (&out)[4], float eps) {
   float acc[4];
 #pragma unroll
@@ -74,7 +76,7 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
   const int head = group * 8 + (threadIdx.x >> 5);
   if (head >= nheads) return;  // whole halves leave together
   const int p = threadIdx.x & 31;
-  const int c0 = head * 128 + 4 * p;
+  const int c0 = head * 128 + 32 * (p >> 3) + block_offset(p);
   const int t0 = ch * CH, t1 = min(T, t0 + CH);
   const int pin = *in_plane;
   float w[4][4];
@@ -139,7 +141,7 @@ __global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __res
                                                               float* __restrict__ beta, int H) {
   const int head = blockIdx.x;
   const int t = threadIdx.x >> 5, p = threadIdx.x & 31;
-  const int c0 = head * 128 + 4 * p;
+  const int c0 = head * 128 + 32 * (p >> 3) + block_offset(p);
   const bool active = t < T;
   const int pin = *in_plane;
   float in[7][4];  // inputs -3 .. 3 of the lane's 4 channels; token t uses in[t .. t+3]
@@ -191,14 +193,13 @@ __global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __res
   st4(y + (size_t)t * C + c0, out[0], out[1], out[2], out[3]);
 }
 
-// l2norm_heads for n = 128: 8 lanes per (token, head); lane q loads channels 4q + 32k (k = 0..3), i.e. the
-// virtual lanes 4q .. 4q+3 of the reference warp with their four values in summation order.
+// l2norm_heads for n = 128: 8 lanes per (token, head); lane q loads channels 4 quad_of_lane(q) + 32k (k = 0..3),
+// i.e. four virtual lanes of the reference warp with their four values in summation order.
 __global__ void __launch_bounds__(256) l2norm128_kernel(float* __restrict__ x, int heads, int T, int stride, float eps) {
   const int item = blockIdx.x * 32 + (threadIdx.x >> 3);
   if (item >= heads * T) return;  // whole 8-lane groups leave together
   const int t = item / heads, hd = item % heads;
-  const int q = threadIdx.x & 7;
-  float* p = x + (size_t)t * stride + (size_t)hd * 128 + 4 * q;
+  float* p = x + (size_t)t * stride + (size_t)hd * 128 + block_offset(threadIdx.x);
   float v[4][4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {

@@ -2,9 +2,10 @@
 // add_norm_rows (residual add + RMSNorm), quantize_q8_1, swiglu_q8, gated_rmsnorm_q8, and the unfused twins
 // rmsnorm / add / swiglu / gated_rmsnorm that the fused == unfused identity is checked against.
 //
-// Row engine (n = 5120): one 256-thread workgroup (4 waves) per row. Thread t loads five float4 at
-// t*4 + k*1024, k = 0..4, so it holds the values of the reference's 1024-thread layout (src/ops.cu:110-121:
-// thread u holds u + k*1024) for the four virtual threads u = 4t .. 4t+3. The per-virtual-thread partial sums
+// Row engine (n = 5120): one 256-thread workgroup (4 waves) per row. Thread t loads five float4, one per
+// 1024-value slice k = 0..4, at the same offset u0 inside each slice (the 32-value block layout of q27h_device.h:
+// u0 = 32 (t / 8) + 4 quad_of_lane(t % 8)), so it holds the values of the reference's 1024-thread layout
+// (src/ops.cu:110-121: thread u holds u + k*1024) for the four virtual threads u = u0 .. u0+3. The per-virtual-thread partial sums
 // of squares, the 32-lane butterflies and the 32-way cross-warp butterfly are then formed from exactly the
 // same operands as the reference (q27h_device.h), while every global access is a 16-byte load or store and a
 // wave moves 1 KiB per instruction.
@@ -25,7 +26,8 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   __shared__ float red[32];
   const int t = threadIdx.x;
   const size_t row = blockIdx.x;
-  const size_t base = row * kRowN + 4 * t;
+  const int off = 32 * (t >> 3) + block_offset(t);  // this thread's 4 values in each 1024-value slice
+  const size_t base = row * kRowN + off;
   float v[5][4];
   float4 wv[5];
 #pragma unroll
@@ -34,7 +36,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
     v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
   }
 #pragma unroll
-  for (int k = 0; k < 5; k++) wv[k] = ld4(w + 4 * t + k * 1024);  // issued before the reduction: no extra round trip
+  for (int k = 0; k < 5; k++) wv[k] = ld4(w + off + k * 1024);  // issued before the reduction: no extra round trip
   if constexpr (MODE != kPlain) {
 #pragma unroll
     for (int k = 0; k < 5; k++) {
@@ -65,7 +67,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   const float wsum = vwarp_sum4(s);
   if ((t & 7) == 0) red[t >> 3] = wsum;
   __syncthreads();
-  const float tot = warp32_sum(red[t & 31]);
+  const float tot = red32_sum(red);
   const float scale = 1.0f / __builtin_sqrtf(tot / (float)kRowN + eps);
 #pragma unroll
   for (int k = 0; k < 5; k++) {
@@ -79,12 +81,9 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 }
 
 // ---------------------------------------------------------------- flat q8_1 producers
-// A 256-thread workgroup covers kFlatU * 1024 consecutive values; thread t handles values 4t .. 4t+3 of each
-// 1024-value chunk (n % 32 == 0, so a q8 block is 8 aligned lanes of one chunk). All loads of a thread are
+// A 256-thread workgroup covers kFlatU * 1024 consecutive values; in each 1024-value chunk thread t handles the 4
+// values at 32 (t / 8) + 4 quad_of_lane(t % 8) (n % 32 == 0, so a q8 block is the 8 lanes of one group). All loads of a thread are
 // issued before any arithmetic so kFlatU * 16 (quantize) or 32 (swiglu) bytes per lane are in flight.
-#ifndef Q27H_PERSIST
-#define Q27H_PERSIST 0
-#endif
 #ifndef Q27H_FLAT_U
 #define Q27H_FLAT_U 2
 #endif
@@ -94,7 +93,7 @@ template <bool SWIGLU>
 __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                       int8_t* __restrict__ xq, float* __restrict__ xd,
                                                       float* __restrict__ xs, size_t n) {
-  const size_t base = (size_t)blockIdx.x * (kFlatU * 1024) + 4 * threadIdx.x;
+  const size_t base = (size_t)blockIdx.x * (kFlatU * 1024) + 32 * (threadIdx.x >> 3) + block_offset(threadIdx.x);
   float4 a[kFlatU], b[kFlatU];
 #pragma unroll
   for (int c = 0; c < kFlatU; c++) {
@@ -118,55 +117,14 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
   }
 }
 
-// Persistent form: gridDim.x workgroups walk the kFlatU * 1024-value tiles with stride gridDim.x, and the loads of
-// the next tile are issued before the current tile is computed (one tile of prefetch per thread).
-template <bool SWIGLU>
-__global__ void __launch_bounds__(256) flat_q8_persist_kernel(const float* __restrict__ g, const float* __restrict__ u,
-                                                              int8_t* __restrict__ xq, float* __restrict__ xd,
-                                                              float* __restrict__ xs, size_t n, size_t ntiles) {
-  float4 a[kFlatU], b[kFlatU], na[kFlatU], nb[kFlatU];
-  size_t tile = blockIdx.x;
-  auto load = [&](size_t tl, float4 (&ra)[kFlatU], float4 (&rb)[kFlatU]) {
-    const size_t base = tl * (kFlatU * 1024) + 4 * threadIdx.x;
-#pragma unroll
-    for (int c = 0; c < kFlatU; c++) {
-      const size_t i0 = base + (size_t)c * 1024;
-      if (i0 < n) {
-        ra[c] = ld4_nt(g + i0);
-        if constexpr (SWIGLU) rb[c] = ld4_nt(u + i0);
-      }
-    }
-  };
-  if (tile < ntiles) load(tile, a, b);
-  for (; tile < ntiles; tile += gridDim.x) {
-    const size_t next = tile + gridDim.x;
-    if (next < ntiles) load(next, na, nb);
-    const size_t base = tile * (kFlatU * 1024) + 4 * threadIdx.x;
-#pragma unroll
-    for (int c = 0; c < kFlatU; c++) {
-      const size_t i0 = base + (size_t)c * 1024;
-      if (i0 >= n) break;  // whole 8-lane groups leave together
-      float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
-      if constexpr (SWIGLU) {
-        const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) y[k] = q27_silu(y[k]) * ub[k];
-      }
-      q8_1_store4(y, xq, xd, xs, i0);
-    }
-#pragma unroll
-    for (int c = 0; c < kFlatU; c++) {
-      a[c] = na[c];
-      if constexpr (SWIGLU) b[c] = nb[c];
-    }
-  }
-}
-
 // ---------------------------------------------------------------- gated RMSNorm -> q8_1 (heads of 128)
-// 32 lanes per head, lane p holds values 4p .. 4p+3; each 32-lane half handles kGatedH consecutive heads (loads
+// 32 lanes per head in the 32-value block layout (4 groups of 8 lanes); each 32-lane half handles kGatedH heads (loads
 // of all of them issued first), a 256-thread workgroup 8 * kGatedH heads. The reference's 128-thread block_sum
 // (4 warps) becomes: per virtual warp (8 lanes) vwarp_sum4, then the second stage over the 4 warp sums with
 // zeros in lanes 4..31, i.e. (w0 + w2) + (w1 + w3) = lane xor 16, then lane xor 8.
+#ifndef Q27H_GATED_SILU_FIRST
+#define Q27H_GATED_SILU_FIRST 1
+#endif
 #ifndef Q27H_GATED_H
 #define Q27H_GATED_H 1
 #endif
@@ -179,23 +137,30 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __re
   const int head0 = (blockIdx.x * 8 + (threadIdx.x >> 5)) * kGatedH;
   if (head0 >= heads) return;  // whole 32-lane halves leave together
   const int p = threadIdx.x & 31;
+  const int off = 32 * (p >> 3) + block_offset(p);
   const int nh = min(kGatedH, heads - head0);
   float4 ov[kGatedH], zv[kGatedH];
 #pragma unroll
   for (int k = 0; k < kGatedH; k++) {
     if (k < nh) {
-      const size_t i0 = (size_t)(head0 + k) * 128 + 4 * p;
+      const size_t i0 = (size_t)(head0 + k) * 128 + off;
       ov[k] = ld4_nt(o + i0);
       zv[k] = ld4_nt(z + i0);
     }
   }
-  const float4 wv = ld4(w + 4 * p);
+  const float4 wv = ld4(w + off);
   const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
   for (int k = 0; k < kGatedH; k++) {
     if (k >= nh) break;
-    const size_t i0 = (size_t)(head0 + k) * 128 + 4 * p;
+    const size_t i0 = (size_t)(head0 + k) * 128 + off;
     const float v[4] = {ov[k].x, ov[k].y, ov[k].z, ov[k].w};
+    const float zz[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
+#if Q27H_GATED_SILU_FIRST
+    float gz[4];  // silu(z) does not depend on the norm: issued first, it overlaps the reduction's lane exchanges
+#pragma unroll
+    for (int c = 0; c < 4; c++) gz[c] = q27_silu(zz[c]);
+#endif
     float s[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) s[c] = v[c] * v[c];
@@ -204,10 +169,14 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __re
     tsum += lane_xor<16>(tsum);
     tsum += lane_xor<8>(tsum);
     const float scale = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
-    const float zz[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
     float y[4];
+#if Q27H_GATED_SILU_FIRST
+#pragma unroll
+    for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * gz[c];
+#else
 #pragma unroll
     for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * q27_silu(zz[c]);
+#endif
     q8_1_store4(y, xq, xd, xs, i0);
   }
 }
@@ -283,18 +252,10 @@ int launch_flat(const char* fn, bool swiglu, const float* g, const float* u, int
   if (!aligned16(g) || (swiglu && !aligned16(u)) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, std::string(fn) + ": inputs need 16-byte and xq 4-byte alignment");
   const size_t blocks = (n + kFlatU * 1024 - 1) / (kFlatU * 1024);
-#if Q27H_PERSIST
-  const size_t grid = blocks < (size_t)Q27H_PERSIST ? blocks : (size_t)Q27H_PERSIST;
-  if (swiglu)
-    hipLaunchKernelGGL(flat_q8_persist_kernel<true>, dim3((unsigned)grid), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n, blocks);
-  else
-    hipLaunchKernelGGL(flat_q8_persist_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n, blocks);
-#else
   if (swiglu)
     hipLaunchKernelGGL(flat_q8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
   else
     hipLaunchKernelGGL(flat_q8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
-#endif
   return check_launch(fn);
 }
 

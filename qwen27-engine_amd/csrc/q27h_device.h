@@ -14,14 +14,17 @@ namespace q27h {
 constexpr int kRowN = 5120;  // hidden size of the row kernels (n must be 5120, src/ops.cu:699)
 
 // ---------------------------------------------------------------- lane exchange
-// Value of lane (lane ^ M), M in {1, 2, 4, 8, 16, 24}: stays inside an aligned group of 32 lanes.
+// Value of lane (lane ^ M), M in {1, 2, 4, 7, 8, 16, 24}: stays inside an aligned group of 32 lanes.
 template <int M>
 __device__ __forceinline__ float lane_xor(float v) {
   const int iv = __builtin_bit_cast(int, v);
   int r;
-  if constexpr (M == 1) r = __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false);        // quad_perm [1,0,3,2]
-  else if constexpr (M == 2) r = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
-  else if constexpr (M == 8) r = __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false);  // row_ror:8 (16-lane rows)
+  // bound_ctrl set: every source lane of these patterns is in range, and the backend can then fold the move into
+  // the consuming add / max as a DPP operand (one instruction instead of two)
+  if constexpr (M == 1) r = __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, true);        // quad_perm [1,0,3,2]
+  else if constexpr (M == 2) r = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+  else if constexpr (M == 8) r = __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, true);  // row_ror:8 (16-lane rows)
+  else if constexpr (M == 7) r = __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, true);  // row_half_mirror: l ^ 7 in 8
   else r = __builtin_amdgcn_ds_swizzle(iv, (M << 10) | 0x1F);                          // bit mode: lane ^ M
   return __builtin_bit_cast(float, r);
 }
@@ -31,12 +34,22 @@ __device__ __forceinline__ float lane_pick(float v) {
   const int iv = __builtin_bit_cast(int, v);
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, (OR << 5) | AND));
 }
-// Value of lane (lane ^ 32): crosses the two halves of the wave (ds_bpermute).
+// Value of lane (lane ^ 32): crosses the two halves of the wave (v_permlane32_swap, then the half's own copy).
 __device__ __forceinline__ float lane_xor32(float v) {
-  const int lane = __lane_id();
   const int iv = __builtin_bit_cast(int, v);
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, iv));
+  const auto pr = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+  return __builtin_bit_cast(float, (__lane_id() & 32) ? (int)pr[0] : (int)pr[1]);
 }
+
+// ---------------------------------------------------------------- lane layout of a 32-value block
+// Eight lanes hold one block of 32 consecutive values, four per lane. Lane q (= lane & 7) holds the four values at
+// 4 * quad_of_lane(q): lanes 0..3 take quads 0..3 and lanes 4..7 quads 7..4. With this order the reference's
+// butterfly over the block's 32 virtual lanes (xor 16, 8, 4, 2, 1) is lane xor 7 (row_half_mirror), lane xor 2,
+// lane xor 1 (quad permutes) and then the lane's own value pairs: DPP operands that fold into the adds. The loads
+// and stores of the 8 lanes still cover the block's 128 bytes exactly.
+__device__ __forceinline__ int quad_of_lane(int q) { return q < 4 ? q : 11 - q; }
+// Offset (in values) of this thread's four values inside its group's 32-value block.
+__device__ __forceinline__ int block_offset(int lane) { return 4 * quad_of_lane(lane & 7); }
 
 // The reference's warp_sum (xor 16, 8, 4, 2, 1 over the 32 lanes of a lane group).
 __device__ __forceinline__ float warp32_sum(float v) {
@@ -195,24 +208,23 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
 
-// q8_1 of 32 consecutive values held by 8 consecutive lanes, 4 values per lane (the lane's values are flat
-// indices i0 .. i0 + 3, i0 % 4 == 0, lanes (i0 / 4) % 8 = 0..7 of an aligned 8-lane group):
-// amax over the block, d = amax / 127, q = roundf(y / d) (0 when amax == 0), xd = fp16(d) as f32 and the
-// optional per-16 sums of the unquantized values in the reference's butterfly order (xor 8, 4, 2, 1 over the
-// 16 virtual lanes = lane xor 2, lane xor 1, then value pairs (0,2)(1,3), then (0,1)).
+// q8_1 of a 32-value block held by the 8 lanes of a group in the block layout above (the lane's values are flat
+// indices i0 .. i0 + 3): amax over the block, d = amax / 127, q = roundf(y / d) (0 when amax == 0), xd = fp16(d)
+// as f32, and the optional per-16 sums of the unquantized values in the reference's butterfly order (xor 8, 4, 2, 1
+// over the 16 virtual lanes = lane xor 2, lane xor 1, then value pairs (0,2)(1,3), then (0,1)); the block's first
+// 16 values sit in lanes 0..3 of the group and the last 16 in lanes 4..7.
 __device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restrict__ xq, float* __restrict__ xd,
                                             float* __restrict__ xs, size_t i0) {
   float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(y[0]), __builtin_fabsf(y[1])),
                                __builtin_fmaxf(__builtin_fabsf(y[2]), __builtin_fabsf(y[3])));
-  amax = __builtin_fmaxf(amax, lane_xor<4>(amax));
+  amax = __builtin_fmaxf(amax, lane_xor<7>(amax));
   amax = __builtin_fmaxf(amax, lane_xor<2>(amax));
   amax = __builtin_fmaxf(amax, lane_xor<1>(amax));
   const float d = amax / 127.0f;
   int q[4] = {0, 0, 0, 0};
   if (amax != 0.0f) q8_round_div4(y, d, q);
   *(uint32_t*)(xq + i0) = pack4_i8(q[0], q[1], q[2], q[3]);
-  const int sub = (int)((i0 >> 2) & 7);
-  if (sub == 0) xd[i0 >> 5] = fp16_round(d);
+  if ((i0 & 31) == 0) xd[i0 >> 5] = fp16_round(d);
   if (xs) {
     float u[4];
 #pragma unroll
@@ -220,21 +232,35 @@ __device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restr
 #pragma unroll
     for (int c = 0; c < 4; c++) u[c] = u[c] + lane_xor<1>(u[c]);
     const float tot = (u[0] + u[2]) + (u[1] + u[3]);
-    if ((sub & 3) == 0) xs[i0 >> 4] = tot;
+    if ((i0 & 15) == 0) xs[i0 >> 4] = tot;
   }
 }
 
-// First stage of the reference block_sum for 32-thread virtual warps whose thread t holds the values of
-// virtual lanes 4 (t & 7) + c, c = 0..3 (8 physical lanes = one virtual warp): xor 16, 8, 4 of the virtual
-// lanes are lane xor 4, 2, 1; xor 2 and 1 pair the lane's own values. Returns the virtual warp's sum.
+// First stage of the reference block_sum for a 32-thread virtual warp held by 8 lanes in the block layout above
+// (lane q holds virtual lanes 4 quad_of_lane(q) + c): virtual xor 16, 8, 4 are lane xor 7, 2, 1, and virtual xor 2
+// and 1 pair the lane's own values. Every lane of the group returns the virtual warp's sum.
 __device__ __forceinline__ float vwarp_sum4(float (&s)[4]) {
 #pragma unroll
-  for (int c = 0; c < 4; c++) s[c] += lane_xor<4>(s[c]);
+  for (int c = 0; c < 4; c++) s[c] += lane_xor<7>(s[c]);
 #pragma unroll
   for (int c = 0; c < 4; c++) s[c] += lane_xor<2>(s[c]);
 #pragma unroll
   for (int c = 0; c < 4; c++) s[c] += lane_xor<1>(s[c]);
   return (s[0] + s[2]) + (s[1] + s[3]);
+}
+
+// The reference's second stage over 32 warp sums red[0..31] (warp_sum: xor 16, 8, 4, 2, 1 of the warp index),
+// evaluated with lane l holding red[(l & 24) | quad_of_lane(l & 7)]: the warp-index xors are then lane xor 16, 8,
+// 7, 2, 1. All 32 lanes of each half-wave return the total.
+__device__ __forceinline__ float red32_sum(const float* red) {
+  const int l = __lane_id() & 31;
+  float v = red[(l & 24) | quad_of_lane(l & 7)];
+  v += lane_xor<16>(v);
+  v += lane_xor<8>(v);
+  v += lane_xor<7>(v);
+  v += lane_xor<2>(v);
+  v += lane_xor<1>(v);
+  return v;
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*)p; }
