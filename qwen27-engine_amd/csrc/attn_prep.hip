@@ -53,11 +53,11 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
     const int hb = hb0 + i;
     if (i < nhw) {
       if (hb < nqh) {
-        xin[i] = ld4(qg + ((size_t)tok * nqh + hb) * 512 + off);
+        xin[i] = ld4_nt(qg + ((size_t)tok * nqh + hb) * 512 + off);
       } else {
         const size_t o = ((size_t)tok * nkvh + (hb - nqh)) * 256 + off;
-        xin[i] = ld4(k + o);
-        vin[i] = ld4(v + o);
+        xin[i] = ld4_nt(k + o);
+        vin[i] = ld4_nt(v + o);
       }
     }
   }
@@ -78,27 +78,31 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
   }
   const bool valid = pos >= 0 && pos < n_ctx;  // uniform over the wave
   const size_t so = (size_t)nkvh * n_ctx * 256;
+  // RMSNorm over the 256 dims, for every head of the group first (independent reductions whose lane exchanges
+  // overlap): 8 virtual warps of 32 (8 lanes each), then ((w0+w4)+(w2+w6)) + ((w1+w5)+(w3+w7))
+  float scale[HPW];
+#pragma unroll
+  for (int i = 0; i < HPW; i++) {
+    float sq[4] = {xin[i].x * xin[i].x, xin[i].y * xin[i].y, xin[i].z * xin[i].z, xin[i].w * xin[i].w};
+    float t = vwarp_sum4(sq);
+    t = t + lane_xor32(t);
+    t += lane_xor<16>(t);
+    t += lane_xor<8>(t);
+    scale[i] = 1.0f / __builtin_sqrtf(t / 256.0f + eps);
+  }
 #pragma unroll
   for (int i = 0; i < HPW; i++) {
     if (i >= nhw) break;
     const int hb = hb0 + i;
     const bool isq = hb < nqh;
     const float x[4] = {xin[i].x, xin[i].y, xin[i].z, xin[i].w};
-    // RMSNorm over the 256 dims: 8 virtual warps of 32 (8 lanes each), then ((w0+w4)+(w2+w6)) + ((w1+w5)+(w3+w7))
-    float s[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) s[c] = x[c] * x[c];
-    float t = vwarp_sum4(s);
-    t = t + lane_xor32(t);
-    t += lane_xor<16>(t);
-    t += lane_xor<8>(t);
-    const float scale = 1.0f / __builtin_sqrtf(t / 256.0f + eps);
+    const float sc = scale[i];
     const float4 wv = isq ? qw : kw;
     const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
     float buf[4], out[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      buf[c] = scale * x[c] * ww[c];
+      buf[c] = sc * x[c] * ww[c];
       out[c] = buf[c];
     }
     // NeoX rotation of (j, j + 32), j < 32: the partner of lane p < 16 is lane p ^ 8

@@ -11,7 +11,7 @@
 #include "q27h_internal.h"
 
 #ifndef Q27H_GDN_CH
-#define Q27H_GDN_CH 16
+#define Q27H_GDN_CH 8
 #endif
 
 namespace q27h {
@@ -101,20 +101,34 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
     s2[0] = r2.x; s2[1] = r2.y; s2[2] = r2.z; s2[3] = r2.w;
   }
   const bool norm = head < n_norm_heads;
+  // software pipeline over the chunk: the conv + SiLU of token t + 1 is issued before the L2 reduction of token t
+  auto conv_next = [&](int t, float (&out)[4]) {
+    const float4 xv = ld4(x + (size_t)t * C + c0);
+    const float xn[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+#if defined(Q27H_DIAG) && (Q27H_DIAG & 2)
+      out[c] = conv4(s0[c], s1[c], s2[c], xn[c], w[c]);
+#else
+      out[c] = q27_silu(conv4(s0[c], s1[c], s2[c], xn[c], w[c]));
+#endif
+      s0[c] = s1[c]; s1[c] = s2[c]; s2[c] = xn[c];
+    }
+  };
+  float cur[4];
+  if (t0 < t1) conv_next(t0, cur);
 #pragma unroll
   for (int i = 0; i < CH; i++) {
     const int t = t0 + i;
     if (t >= t1) break;
-    const float4 xv = ld4(x + (size_t)t * C + c0);
-    const float xn[4] = {xv.x, xv.y, xv.z, xv.w};
-    float out[4];
+    float nxt[4];
+    if (t + 1 < t1) conv_next(t + 1, nxt);
+#if !(defined(Q27H_DIAG) && (Q27H_DIAG & 1))
+    if (norm) l2_head_lanes(cur, eps);
+#endif
+    st4(y + (size_t)t * C + c0, cur[0], cur[1], cur[2], cur[3]);
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      out[c] = q27_silu(conv4(s0[c], s1[c], s2[c], xn[c], w[c]));
-      s0[c] = s1[c]; s1[c] = s2[c]; s2[c] = xn[c];
-    }
-    if (norm) l2_head_lanes(out, eps);
-    st4(y + (size_t)t * C + c0, out[0], out[1], out[2], out[3]);
+    for (int c = 0; c < 4; c++) cur[c] = nxt[c];
   }
   if (!norm) {
     const int hv = head - n_norm_heads;

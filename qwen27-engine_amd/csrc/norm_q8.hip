@@ -144,8 +144,8 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __re
   for (int k = 0; k < kGatedH; k++) {
     if (k < nh) {
       const size_t i0 = (size_t)(head0 + k) * 128 + off;
+      zv[k] = ld4_nt(z + i0);  // z first: silu(z) is computed first
       ov[k] = ld4_nt(o + i0);
-      zv[k] = ld4_nt(z + i0);
     }
   }
   const float4 wv = ld4(w + off);
