@@ -2,11 +2,12 @@
 // (gdn_conv_l2, T <= 4 with state snapshots) and prefill (gdn_conv_prefill, M tokens, state plane flip), plus the
 // unfused twins gdn_conv / gdn_gates / l2norm_heads.
 //
-// Fused layout: 32 lanes (half a wave) per (head of 128 channels, token or chunk of tokens); lane p owns 4
-// consecutive channels (the 32-value block layout of q27h_device.h), so every token row of a head is one 512-byte load and store, and in prefill the conv window of the
-// last three inputs stays in registers while the lanes walk the chunk's tokens. The L2 norm reproduces the reference's
-// warp-per-head order (src/ops.cu:318-330, 442-446): virtual lane v sums y[v]^2, y[v+32]^2, y[v+64]^2, y[v+96]^2
-// in that order, then the xor butterfly; those four values sit in lanes (p & 7) + 8k, fetched with ds_swizzle.
+// Fused layout: 32 lanes (half a wave) per (head of 128 channels, token or chunk of tokens). Lane p owns the
+// channels v + 32k, k = 0..3, of the head, with v = (p & 24) | quad_of_lane(p & 7): the reference's L2-norm lane v
+// (src/ops.cu:318-330, 442-446: lane v sums y[v]^2, y[v+32]^2, y[v+64]^2, y[v+96]^2 in that order, then the xor
+// butterfly) is then this lane, the sum is in-lane, and the butterfly's xor 16, 8, 4, 2, 1 are lane xor 16, 8, 7,
+// 2, 1. Each of the four channel loads / stores of a token covers 128 contiguous bytes over the 32 lanes. In prefill
+// the conv window of the last three inputs stays in registers while the lanes walk the chunk's tokens.
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
@@ -26,27 +27,24 @@ __device__ __forceinline__ float conv4(float s0, float s1, float s2, float xn, c
   return sum;
 }
 
-// L2 norm of one 128-channel head held by a 32-lane half in the 32-value block layout (lane p holds channels
-// 32 (p / 8) + 4 quad_of_lane(p % 8) + c): the reference lane v's values v, v + 32, v + 64, v + 96 sit in lanes
-// (p & 7) + 8k, gathered in that order, then the virtual warp butterfly.
+// L2 norm of one 128-channel head held by a 32-lane half, out[k] = channel v + 32k of lane p (layout above).
 __device__ __forceinline__ void l2_head_lanes(float (&out)[4], float eps) {
-  float acc[4];
+  float acc = 0.0f;
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const float sq = out[c] * out[c];
-    float a = 0.0f;
-    a += lane_pick<7, 0>(sq);
-    a += lane_pick<7, 8>(sq);
-    a += lane_pick<7, 16>(sq);
-    a += lane_pick<7, 24>(sq);
-    acc[c] = a;
-  }
-  const float tot = vwarp_sum4(acc);
-  const float scale = 1.0f / __builtin_sqrtf(tot / 128.0f + eps / 128.0f);
+  for (int k = 0; k < 4; k++) acc += out[k] * out[k];
+  acc += lane_xor<16>(acc);
+  acc += lane_xor<8>(acc);
+  acc += lane_xor<7>(acc);
+  acc += lane_xor<2>(acc);
+  acc += lane_xor<1>(acc);
+  const float scale = 1.0f / __builtin_sqrtf(acc / 128.0f + eps / 128.0f);
   const float post = 1.0f / __builtin_sqrtf(128.0f);
 #pragma unroll
-  for (int c = 0; c < 4; c++) out[c] = (out[c] * scale) * post;
+  for (int k = 0; k < 4; k++) out[k] = (out[k] * scale) * post;
 }
+
+// The reference L2 lane held by lane p of a 32-lane half (see the layout note at the top of the file).
+__device__ __forceinline__ int l2_lane(int p) { return (p & 24) | quad_of_lane(p & 7); }
 
 __device__ __forceinline__ void gate_one(const float* __restrict__ a, const float* __restrict__ b,
                                          const float* __restrict__ ssm_a, const float* __restrict__ dt_bias,
@@ -76,43 +74,40 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
   const int head = group * 8 + (threadIdx.x >> 5);
   if (head >= nheads) return;  // whole halves leave together
   const int p = threadIdx.x & 31;
-  const int c0 = head * 128 + 32 * (p >> 3) + block_offset(p);
+  const int cb = head * 128 + l2_lane(p);  // channels cb + 32k
   const int t0 = ch * CH, t1 = min(T, t0 + CH);
   const int pin = *in_plane;
   float w[4][4];
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const float4 wv = ld4(cw + 4 * (size_t)(c0 + c));
-    w[c][0] = wv.x; w[c][1] = wv.y; w[c][2] = wv.z; w[c][3] = wv.w;
+  for (int k = 0; k < 4; k++) {
+    const float4 wv = ld4(cw + 4 * (size_t)(cb + 32 * k));
+    w[k][0] = wv.x; w[k][1] = wv.y; w[k][2] = wv.z; w[k][3] = wv.w;
   }
   // conv window: s0, s1, s2 = inputs t0-3, t0-2, t0-1 (state plane `pin` before the batch)
   float s0[4], s1[4], s2[4];
   if (t0 == 0) {
-    const float* st = planes + ((size_t)pin * C + c0) * 3;  // 12 floats: channel c taps at 3c .. 3c+2
-    const float4 q0 = ld4(st), q1 = ld4(st + 4), q2 = ld4(st + 8);
-    const float sv[12] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w};
 #pragma unroll
-    for (int c = 0; c < 4; c++) { s0[c] = sv[3 * c]; s1[c] = sv[3 * c + 1]; s2[c] = sv[3 * c + 2]; }
+    for (int k = 0; k < 4; k++) {
+      const float* st = planes + ((size_t)pin * C + cb + 32 * k) * 3;
+      s0[k] = st[0]; s1[k] = st[1]; s2[k] = st[2];
+    }
   } else {
-    const float4 r0 = ld4(x + (size_t)(t0 - 3) * C + c0), r1 = ld4(x + (size_t)(t0 - 2) * C + c0),
-                 r2 = ld4(x + (size_t)(t0 - 1) * C + c0);
-    s0[0] = r0.x; s0[1] = r0.y; s0[2] = r0.z; s0[3] = r0.w;
-    s1[0] = r1.x; s1[1] = r1.y; s1[2] = r1.z; s1[3] = r1.w;
-    s2[0] = r2.x; s2[1] = r2.y; s2[2] = r2.z; s2[3] = r2.w;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      s0[k] = x[(size_t)(t0 - 3) * C + cb + 32 * k];
+      s1[k] = x[(size_t)(t0 - 2) * C + cb + 32 * k];
+      s2[k] = x[(size_t)(t0 - 1) * C + cb + 32 * k];
+    }
   }
   const bool norm = head < n_norm_heads;
   // software pipeline over the chunk: the conv + SiLU of token t + 1 is issued before the L2 reduction of token t
   auto conv_next = [&](int t, float (&out)[4]) {
-    const float4 xv = ld4(x + (size_t)t * C + c0);
-    const float xn[4] = {xv.x, xv.y, xv.z, xv.w};
+    const float* xr = x + (size_t)t * C + cb;
+    const float xn[4] = {xr[0], xr[32], xr[64], xr[96]};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-#if defined(Q27H_DIAG) && (Q27H_DIAG & 2)
-      out[c] = conv4(s0[c], s1[c], s2[c], xn[c], w[c]);
-#else
-      out[c] = q27_silu(conv4(s0[c], s1[c], s2[c], xn[c], w[c]));
-#endif
-      s0[c] = s1[c]; s1[c] = s2[c]; s2[c] = xn[c];
+    for (int k = 0; k < 4; k++) {
+      out[k] = q27_silu(conv4(s0[k], s1[k], s2[k], xn[k], w[k]));
+      s0[k] = s1[k]; s1[k] = s2[k]; s2[k] = xn[k];
     }
   };
   float cur[4];
@@ -123,22 +118,22 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
     if (t >= t1) break;
     float nxt[4];
     if (t + 1 < t1) conv_next(t + 1, nxt);
-#if !(defined(Q27H_DIAG) && (Q27H_DIAG & 1))
     if (norm) l2_head_lanes(cur, eps);
-#endif
-    st4(y + (size_t)t * C + c0, cur[0], cur[1], cur[2], cur[3]);
+    float* yr = y + (size_t)t * C + cb;
+    yr[0] = cur[0]; yr[32] = cur[1]; yr[64] = cur[2]; yr[96] = cur[3];
 #pragma unroll
-    for (int c = 0; c < 4; c++) cur[c] = nxt[c];
+    for (int k = 0; k < 4; k++) cur[k] = nxt[k];
   }
   if (!norm) {
     const int hv = head - n_norm_heads;
     for (int t = t0 + p; t < t1; t += 32) gate_one(a, b, ssm_a, dt_bias, g, beta, t, H, hv);
   }
   if (t1 == T) {  // state after the batch: inputs T-3 .. T-1 (from the old state when T < 3)
-    float* o = planes + ((size_t)(pin == 0 ? 1 : 0) * C + c0) * 3;
-    st4(o, s0[0], s1[0], s2[0], s0[1]);
-    st4(o + 4, s1[1], s2[1], s0[2], s1[2]);
-    st4(o + 8, s2[2], s0[3], s1[3], s2[3]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      float* o = planes + ((size_t)(pin == 0 ? 1 : 0) * C + cb + 32 * k) * 3;
+      o[0] = s0[k]; o[1] = s1[k]; o[2] = s2[k];
+    }
   }
 }
 
@@ -155,56 +150,51 @@ __global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __res
                                                               float* __restrict__ beta, int H) {
   const int head = blockIdx.x;
   const int t = threadIdx.x >> 5, p = threadIdx.x & 31;
-  const int c0 = head * 128 + 32 * (p >> 3) + block_offset(p);
+  const int cb = head * 128 + l2_lane(p);  // channels cb + 32k
   const bool active = t < T;
   const int pin = *in_plane;
   float in[7][4];  // inputs -3 .. 3 of the lane's 4 channels; token t uses in[t .. t+3]
-  {
-    const float* st = planes + ((size_t)pin * C + c0) * 3;
-    const float4 q0 = ld4(st), q1 = ld4(st + 4), q2 = ld4(st + 8);
-    const float sv[12] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w};
 #pragma unroll
-    for (int c = 0; c < 4; c++) { in[0][c] = sv[3 * c]; in[1][c] = sv[3 * c + 1]; in[2][c] = sv[3 * c + 2]; }
+  for (int k = 0; k < 4; k++) {
+    const float* st = planes + ((size_t)pin * C + cb + 32 * k) * 3;
+    in[0][k] = st[0]; in[1][k] = st[1]; in[2][k] = st[2];
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    if (r < T && r <= t) {
-      const float4 xv = ld4(x + (size_t)r * C + c0);
-      in[3 + r][0] = xv.x; in[3 + r][1] = xv.y; in[3 + r][2] = xv.z; in[3 + r][3] = xv.w;
-    } else {
 #pragma unroll
-      for (int c = 0; c < 4; c++) in[3 + r][c] = 0.0f;
-    }
+    for (int k = 0; k < 4; k++) in[3 + r][k] = (r < T && r <= t) ? x[(size_t)r * C + cb + 32 * k] : 0.0f;
   }
   float w[4][4];
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const float4 wv = ld4(cw + 4 * (size_t)(c0 + c));
-    w[c][0] = wv.x; w[c][1] = wv.y; w[c][2] = wv.z; w[c][3] = wv.w;
+  for (int k = 0; k < 4; k++) {
+    const float4 wv = ld4(cw + 4 * (size_t)(cb + 32 * k));
+    w[k][0] = wv.x; w[k][1] = wv.y; w[k][2] = wv.z; w[k][3] = wv.w;
   }
   // window of token t (registers, selected with constant indices)
   float s0[4], s1[4], s2[4], xn[4];
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    s0[c] = t == 0 ? in[0][c] : t == 1 ? in[1][c] : t == 2 ? in[2][c] : in[3][c];
-    s1[c] = t == 0 ? in[1][c] : t == 1 ? in[2][c] : t == 2 ? in[3][c] : in[4][c];
-    s2[c] = t == 0 ? in[2][c] : t == 1 ? in[3][c] : t == 2 ? in[4][c] : in[5][c];
-    xn[c] = t == 0 ? in[3][c] : t == 1 ? in[4][c] : t == 2 ? in[5][c] : in[6][c];
+  for (int k = 0; k < 4; k++) {
+    s0[k] = t == 0 ? in[0][k] : t == 1 ? in[1][k] : t == 2 ? in[2][k] : in[3][k];
+    s1[k] = t == 0 ? in[1][k] : t == 1 ? in[2][k] : t == 2 ? in[3][k] : in[4][k];
+    s2[k] = t == 0 ? in[2][k] : t == 1 ? in[3][k] : t == 2 ? in[4][k] : in[5][k];
+    xn[k] = t == 0 ? in[3][k] : t == 1 ? in[4][k] : t == 2 ? in[5][k] : in[6][k];
   }
   __syncthreads();  // every plane read of the workgroup is consumed before any snapshot write
   if (!active) return;
   float out[4];
 #pragma unroll
-  for (int c = 0; c < 4; c++) out[c] = q27_silu(conv4(s0[c], s1[c], s2[c], xn[c], w[c]));
+  for (int k = 0; k < 4; k++) out[k] = q27_silu(conv4(s0[k], s1[k], s2[k], xn[k], w[k]));
   if (snapshots || t == T - 1) {
-    float* o = planes + ((size_t)t * C + c0) * 3;
-    st4(o, s1[0], s2[0], xn[0], s1[1]);
-    st4(o + 4, s2[1], xn[1], s1[2], s2[2]);
-    st4(o + 8, xn[2], s1[3], s2[3], xn[3]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      float* o = planes + ((size_t)t * C + cb + 32 * k) * 3;
+      o[0] = s1[k]; o[1] = s2[k]; o[2] = xn[k];
+    }
   }
   if (head < n_norm_heads) l2_head_lanes(out, eps);
   else if (p == 0) gate_one(a, b, ssm_a, dt_bias, g, beta, t, H, head - n_norm_heads);
-  st4(y + (size_t)t * C + c0, out[0], out[1], out[2], out[3]);
+  float* yr = y + (size_t)t * C + cb;
+  yr[0] = out[0]; yr[32] = out[1]; yr[64] = out[2]; yr[96] = out[3];
 }
 
 // l2norm_heads for n = 128: 8 lanes per (token, head); lane q loads channels 4 quad_of_lane(q) + 32k (k = 0..3),
