@@ -7,12 +7,18 @@
 // (src/ops.cu:318-330, 442-446: lane v sums y[v]^2, y[v+32]^2, y[v+64]^2, y[v+96]^2 in that order, then the xor
 // butterfly) is then this lane, the sum is in-lane, and the butterfly's xor 16, 8, 4, 2, 1 are lane xor 16, 8, 7,
 // 2, 1. Each of the four channel loads / stores of a token covers 128 contiguous bytes over the 32 lanes. In prefill
-// the conv window of the last three inputs stays in registers while the lanes walk the chunk's tokens.
+// the conv window of the last three inputs stays in registers while the lanes walk the span's tokens.
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
 #ifndef Q27H_GDN_CH
 #define Q27H_GDN_CH 8
+#endif
+#ifndef Q27H_GDN_FAST_SILU
+#define Q27H_GDN_FAST_SILU 1
+#endif
+#ifndef Q27H_GDN_SPAN
+#define Q27H_GDN_SPAN 8
 #endif
 
 namespace q27h {
@@ -54,29 +60,44 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
   g[i] = q27_softplus(a[i] + dt_bias[hv]) * ssm_a[hv];
 }
 
-// Prefill: 32 lanes per (head of 128 channels, chunk of CH tokens), a workgroup = 8 neighbouring heads of one
-// chunk. The conv window of a chunk starts with the 3 rows before it, which the previous chunk of the same heads
-// has just read: workgroups are numbered so that each XCD (workgroup id mod 8) walks a contiguous range of
-// (head group, chunk) tiles in chunk order, and those rows are L2 hits instead of HBM re-reads.
-template <int CH>
+// Prefill: 32 lanes per (head of 128 channels, span of SPAN tokens), a workgroup = 8 neighbouring heads of one
+// span. The lanes walk the span in batches of CH tokens, the rows of the next batch loaded before the current one is
+// computed. The conv window of a span starts with the 3 rows before it. With SPAN == CH (the default, 8) a span
+// loads all its rows first, so its last 3 rows are read at the same moment as the next span (the next tile of the
+// same XCD in the XCD-major order) reads them as its window: L2 hits, and the kernel's HBM reads stay within 4% of
+// the single pass over the input. Longer spans cut that re-read but leave too few waves to cover the latency.
+template <int CH, int SPAN>
 __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __restrict__ x, const float* __restrict__ cw,
                                                                float* __restrict__ planes, const int* __restrict__ in_plane,
                                                                float* __restrict__ y, int C, int T, int n_norm_heads,
                                                                float eps, const float* __restrict__ a,
                                                                const float* __restrict__ b, const float* __restrict__ ssm_a,
                                                                const float* __restrict__ dt_bias, float* __restrict__ g,
-                                                               float* __restrict__ beta, int H, int nchunks, int tiles_per_xcd) {
+                                                               float* __restrict__ beta, int H, int nspans, int tiles_per_xcd) {
+  static_assert(SPAN % CH == 0 && SPAN >= 3, "a span is whole batches and covers the 3-input window");
   const int nheads = C / 128;
   const int ngroups = (nheads + 7) / 8;
   const int tile = (blockIdx.x & 7) * tiles_per_xcd + (blockIdx.x >> 3);  // XCD-major order of the tiles
-  if (tile >= ngroups * nchunks) return;
-  const int group = tile / nchunks, ch = tile % nchunks;
+  if (tile >= ngroups * nspans) return;
+  const int group = tile / nspans, sp = tile % nspans;
   const int head = group * 8 + (threadIdx.x >> 5);
   if (head >= nheads) return;  // whole halves leave together
   const int p = threadIdx.x & 31;
   const int cb = head * 128 + l2_lane(p);  // channels cb + 32k
-  const int t0 = ch * CH, t1 = min(T, t0 + CH);
+  const int t0 = sp * SPAN, t1 = min(T, t0 + SPAN);
   const int pin = *in_plane;
+  auto load_batch = [&](int tb, float (&dst)[CH][4]) {
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+      if (tb + i < t1) {
+        const float* xr = x + (size_t)(tb + i) * C + cb;
+#pragma unroll
+        for (int k = 0; k < 4; k++) dst[i][k] = xr[32 * k];
+      }
+    }
+  };
+  float xb[CH][4];
+  load_batch(t0, xb);
   float w[4][4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -100,29 +121,36 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
     }
   }
   const bool norm = head < n_norm_heads;
-  // software pipeline over the chunk: the conv + SiLU of token t + 1 is issued before the L2 reduction of token t
-  auto conv_next = [&](int t, float (&out)[4]) {
-    const float* xr = x + (size_t)t * C + cb;
-    const float xn[4] = {xr[0], xr[32], xr[64], xr[96]};
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      out[k] = q27_silu(conv4(s0[k], s1[k], s2[k], xn[k], w[k]));
-      s0[k] = s1[k]; s1[k] = s2[k]; s2[k] = xn[k];
+  for (int j = 0; j < SPAN / CH; j++) {
+    const int tb = t0 + j * CH;
+    if (tb >= t1) break;
+    float xn[CH][4];
+    if (j + 1 < SPAN / CH && tb + CH < t1) load_batch(tb + CH, xn);
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+      const int t = tb + i;
+      if (t >= t1) break;
+      float cv[4], cur[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        cv[k] = conv4(s0[k], s1[k], s2[k], xb[i][k], w[k]);
+        s0[k] = s1[k]; s1[k] = s2[k]; s2[k] = xb[i][k];
+      }
+#if Q27H_GDN_FAST_SILU
+      q27_silu_n(cv, cur);
+#else
+#pragma unroll
+      for (int k = 0; k < 4; k++) cur[k] = q27_silu(cv[k]);
+#endif
+      if (norm) l2_head_lanes(cur, eps);
+      float* yr = y + (size_t)t * C + cb;
+      yr[0] = cur[0]; yr[32] = cur[1]; yr[64] = cur[2]; yr[96] = cur[3];
     }
-  };
-  float cur[4];
-  if (t0 < t1) conv_next(t0, cur);
 #pragma unroll
-  for (int i = 0; i < CH; i++) {
-    const int t = t0 + i;
-    if (t >= t1) break;
-    float nxt[4];
-    if (t + 1 < t1) conv_next(t + 1, nxt);
-    if (norm) l2_head_lanes(cur, eps);
-    float* yr = y + (size_t)t * C + cb;
-    yr[0] = cur[0]; yr[32] = cur[1]; yr[64] = cur[2]; yr[96] = cur[3];
+    for (int i = 0; i < CH; i++)
 #pragma unroll
-    for (int k = 0; k < 4; k++) cur[k] = nxt[k];
+      for (int k = 0; k < 4; k++) xb[i][k] = xn[i][k];
   }
   if (!norm) {
     const int hv = head - n_norm_heads;
@@ -181,9 +209,10 @@ __global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __res
   }
   __syncthreads();  // every plane read of the workgroup is consumed before any snapshot write
   if (!active) return;
-  float out[4];
+  float cv[4], out[4];
 #pragma unroll
-  for (int k = 0; k < 4; k++) out[k] = q27_silu(conv4(s0[k], s1[k], s2[k], xn[k], w[k]));
+  for (int k = 0; k < 4; k++) cv[k] = conv4(s0[k], s1[k], s2[k], xn[k], w[k]);
+  q27_silu_n(cv, out);
   if (snapshots || t == T - 1) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -307,12 +336,13 @@ extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* plan
   if (int e = check_fused("gdn_conv_prefill", x, w, planes, in_plane, y, C, M, n_norm_heads, H, a, b, ssm_a, dt_bias, g, beta))
     return e;
   if (M == 0) return Q27H_OK;
-  constexpr int chunk = Q27H_GDN_CH;  // tokens per half-wave; >= 3 so a chunk's window never reaches past the previous chunk
-  const int nchunks = (M + chunk - 1) / chunk;
-  const long tiles = (long)((C / 128 + 7) / 8) * nchunks;
+  constexpr int span = Q27H_GDN_SPAN;  // tokens per half-wave
+  const int nspans = (M + span - 1) / span;
+  const long tiles = (long)((C / 128 + 7) / 8) * nspans;
   const int tiles_per_xcd = (int)((tiles + 7) / 8);
-  hipLaunchKernelGGL((gdn_conv_prefill_kernel<chunk>), dim3((unsigned)(8 * tiles_per_xcd)), dim3(256), 0, stream_of(s), x, w,
-                     planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, nchunks, tiles_per_xcd);
+  hipLaunchKernelGGL((gdn_conv_prefill_kernel<Q27H_GDN_CH, span>), dim3((unsigned)(8 * tiles_per_xcd)), dim3(256), 0,
+                     stream_of(s), x, w, planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H,
+                     nspans, tiles_per_xcd);
   return check_launch("gdn_conv_prefill");
 }
 

@@ -110,8 +110,10 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
     float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
     if constexpr (SWIGLU) {
       const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
+      float sg[4];
+      q27_silu_n(y, sg);
 #pragma unroll
-      for (int k = 0; k < 4; k++) y[k] = q27_silu(y[k]) * ub[k];
+      for (int k = 0; k < 4; k++) y[k] = sg[k] * ub[k];
     }
     q8_1_store4(y, xq, xd, xs, i0);
   }
@@ -159,7 +161,7 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __re
 #if Q27H_GATED_SILU_FIRST
     float gz[4];  // silu(z) does not depend on the norm: issued first, it overlaps the reduction's lane exchanges
 #pragma unroll
-    for (int c = 0; c < 4; c++) gz[c] = q27_silu(zz[c]);
+    for (int c = 0; c < 4; c++) gz[c] = q27_silu(zz[c]);  // branch-free form: a branch here would end the overlap
 #endif
     float s[4];
 #pragma unroll
@@ -205,7 +207,12 @@ __global__ void add_kernel(const float* __restrict__ x, const float* __restrict_
 
 __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = q27_silu(g[i]) * u[i];
+  if (i < n) {
+    const float gi[1] = {g[i]};
+    float sg[1];
+    q27_silu_n(gi, sg);
+    y[i] = sg[0] * u[i];
+  }
 }
 
 __global__ void set_int_kernel(int* p, int v) { *p = v; }

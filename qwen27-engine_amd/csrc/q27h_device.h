@@ -91,12 +91,10 @@ __device__ __forceinline__ float bf16_to_f(uint16_t b) { return __builtin_bit_ca
 // ---------------------------------------------------------------- transcendental functions
 // exp: Cody-Waite reduction x = k ln2 + r, degree-7 Taylor polynomial of e^r (Horner, fma), ldexp.
 // Same operations and constants as the CPU checker (Muller, Elementary Functions, ch. 11).
-__device__ __forceinline__ float q27_expf(float x) {
-  // Branch-free: the polynomial is evaluated on a clamped argument and the out-of-range results are selected
-  // afterwards, giving the same values as the early-return form of the CPU checker.
-  const float xc = __builtin_fminf(__builtin_fmaxf(x, -103.972084f), 88.7228394f);
-  const float k = __builtin_rintf(xc * 1.44269502f);
-  float r = __builtin_fmaf(-k, 0.693145752f, xc);
+// The reduction, polynomial and scaling of q27_expf, valid where no clamp or special case applies (|x| <= 87).
+__device__ __forceinline__ float q27_expf_core(float x) {
+  const float k = __builtin_rintf(x * 1.44269502f);
+  float r = __builtin_fmaf(-k, 0.693145752f, x);
   r = __builtin_fmaf(-k, 1.42860677e-06f, r);
   float p = 1.98412698e-4f;
   p = __builtin_fmaf(p, r, 1.38888889e-3f);
@@ -106,10 +104,32 @@ __device__ __forceinline__ float q27_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  float e = __builtin_ldexpf(p, (int)k);
+  return __builtin_ldexpf(p, (int)k);
+}
+
+__device__ __forceinline__ float q27_expf(float x) {
+  // Branch-free: the polynomial is evaluated on a clamped argument and the out-of-range results are selected
+  // afterwards, giving the same values as the early-return form of the CPU checker.
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -103.972084f), 88.7228394f);
+  float e = q27_expf_core(xc);
   e = x > 88.7228394f ? __builtin_huge_valf() : e;
   e = x < -103.972084f ? 0.0f : e;
   return x != x ? x + x : e;
+}
+
+// n / d, correctly rounded, for 2^-60 <= |n| <= 2^7 and 1 <= d <= 2^87. This is gfx9's IEEE division sequence
+// (reciprocal, one Newton step, quotient, two residual corrections) without its range scaling and special-case
+// fix-up, which leave every operand unchanged in this range (no operand, residual or quotient comes near the
+// subnormal or overflow range), so the result is bit-identical to n / d.
+__device__ __forceinline__ float div_in_range(float n, float d) {
+  const float y0 = __builtin_amdgcn_rcpf(d);
+  const float e = __builtin_fmaf(-d, y0, 1.0f);
+  const float y = __builtin_fmaf(e, y0, y0);
+  const float q0 = n * y;
+  const float r0 = __builtin_fmaf(-d, q0, n);
+  const float q1 = __builtin_fmaf(r0, y, q0);
+  const float r1 = __builtin_fmaf(-d, q1, n);
+  return __builtin_fmaf(r1, y, q1);
 }
 
 // log for the softplus gate: x = 2^e m, m in [sqrt(1/2), sqrt(2)), s = f / (2 + f), log m = 2 atanh(s) as an
@@ -139,7 +159,27 @@ __device__ __forceinline__ float q27_logf(float x) {
   return __builtin_fmaf(fe, 0.693145752f, __builtin_fmaf(fe, 1.42860677e-06f, logm));
 }
 
+// silu(x) = x / (1 + e^-x). For 2^-60 <= |x| <= 60 the exp needs no clamp and the division is in div_in_range's
+// range (1 + e^-x <= 2^87); other arguments (zeros, subnormals, large or non-finite values) take the general path.
 __device__ __forceinline__ float q27_silu(float x) { return x / (1.0f + q27_expf(-x)); }
+__device__ __forceinline__ bool silu_fast_ok(float x) {
+  const float ax = __builtin_fabsf(x);
+  return ax >= 0x1p-60f && ax <= 60.0f;
+}
+// N values at once, one branch for the lanes with an argument outside the fast range.
+template <int N>
+__device__ __forceinline__ void q27_silu_n(const float (&x)[N], float (&out)[N]) {
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < N; k++) {
+    out[k] = div_in_range(x[k], 1.0f + q27_expf_core(-x[k]));
+    ok &= silu_fast_ok(x[k]);
+  }
+  if (!ok) {
+#pragma unroll
+    for (int k = 0; k < N; k++) out[k] = q27_silu(x[k]);
+  }
+}
 __device__ __forceinline__ float q27_sigmoid(float x) { return 1.0f / (1.0f + q27_expf(-x)); }
 __device__ __forceinline__ float q27_softplus(float x) { return x > 20.0f ? x : q27_logf(1.0f + q27_expf(x)); }
 

@@ -180,6 +180,31 @@ def test_gated_rmsnorm_q8(q27, oracle, T, heads):
         assert_bits_equal(T.down(got), want, what)
 
 
+# ---------------------------------------------------------------- silu over a sweep of float32 bit patterns
+def test_silu_bit_pattern_sweep(q27, oracle, T):
+    """silu(g) * 1 through the unfused swiglu: every 61st float32 bit pattern (about 70 million values: both
+    signs, subnormals, zeros, infinities), plus the neighbours of the fast range's edges 2^-60 and 60. The
+    kernels compute silu with a division without range scaling for 2^-60 <= |x| <= 60 and the general one elsewhere; both
+    must give the oracle's bits. NaN inputs and outputs only have to be NaN (payloads are not specified)."""
+    say("silu bit-pattern sweep")
+    pats = np.arange(0, 1 << 32, 61, dtype=np.uint64).astype(np.uint32)
+    edges = []
+    for e in (np.float32(2.0 ** -60), np.float32(60.0)):
+        b = int(np.array(e).view(np.uint32))
+        edges += list(range(b - 64, b + 65))
+    edges = np.array(edges, np.uint32)
+    pats = np.concatenate([pats, edges, edges | np.uint32(0x80000000)])
+    g = pats.view(np.float32)
+    u = np.ones_like(g)
+    y = T.empty(g.size)
+    q27.ops.swiglu(T.up(g), T.up(u), y, g.size)
+    got = T.down(y)
+    want = oracle.swiglu(g, u)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan), "silu: NaN positions differ"
+    assert_bits_equal(got[~nan], want[~nan], "silu sweep")
+
+
 # ---------------------------------------------------------------- unfused twins and the fused == unfused identity
 def test_unfused_twins(q27, oracle, T):
     say("unfused rmsnorm / add / swiglu / gated_rmsnorm / gdn_gates / gdn_conv")
@@ -258,7 +283,7 @@ def test_gdn_conv_l2_decode(q27, oracle, T, Tn, pin, snap):
         assert_bits_equal(T.down(got), want, what)
 
 
-@pytest.mark.parametrize("M,pin", [(2048, 0), (4099, 1), (1, 0), (2, 1), (3, 0), (17, 1), (33, 0)])
+@pytest.mark.parametrize("M,pin", [(2048, 0), (4099, 1), (1, 0), (2, 1), (3, 0), (17, 1), (33, 0), (70, 1), (129, 0)])
 def test_gdn_conv_prefill(q27, oracle, T, M, pin):
     say(f"gdn_conv_prefill M={M} in_plane={pin}")
     r = cd.rng(70 + M)
