@@ -20,8 +20,10 @@ struct RopeFreqs {
 };
 
 
-// One wave per (token, group of HPW consecutive heads): HPW = 4 for batches (the 28 heads of a token are 7 waves),
-// HPW = 1 for a few tokens, where the shorter chain per wave matters more than loads in flight. The 32 rotary angles of the token are evaluated
+// One wave per (token, group of HPW heads): HPW = 4 for batches (the 28 heads of a token are 7 waves, wave w taking
+// heads w, w + 7, w + 14, w + 21, so the 4 K heads with their q8/f16 cache work are spread over 4 waves instead of
+// making one wave the straggler), HPW = 1 for a few tokens, where the shorter chain per wave matters more than loads
+// in flight. The 32 rotary angles of the token are evaluated
 // once per wave (lane j < 32 takes pair j) and handed to the lanes that need them with ds_bpermute; the head
 // vectors of the whole group are loaded before any arithmetic.
 #ifndef Q27H_ATTN_HPW
@@ -38,37 +40,49 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
                                                         const int* __restrict__ rdelta) {
   const int nh = nqh + nkvh;
   const int wpt = (nh + HPW - 1) / HPW;  // waves per token
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar registers
   if (wave >= T * wpt) return;  // whole waves leave together
   const int tok = wave / wpt;
-  const int hb0 = (wave % wpt) * HPW;
-  const int nhw = min(HPW, nh - hb0);
+  const int hw = wave % wpt;  // heads hw, hw + wpt, hw + 2 wpt, ...: the K heads (the last ones) fall in different waves
+  const int nhw = (nh - hw + wpt - 1) / wpt;
   const int p = threadIdx.x & 63;
   const int off = 32 * (p >> 3) + block_offset(p);  // this lane's 4 head dims (32-value block layout)
   const int pos = *dpos0 + tok;  // cache row
-  // ---- loads of the whole group
+  // ---- loads of the whole group first, branch-free (a missing head of the last group re-reads head hw)
   float4 xin[HPW], vin[HPW];
 #pragma unroll
   for (int i = 0; i < HPW; i++) {
-    const int hb = hb0 + i;
-    if (i < nhw) {
-      if (hb < nqh) {
-        xin[i] = ld4_nt(qg + ((size_t)tok * nqh + hb) * 512 + off);
-      } else {
-        const size_t o = ((size_t)tok * nkvh + (hb - nqh)) * 256 + off;
-        xin[i] = ld4_nt(k + o);
-        vin[i] = ld4_nt(v + o);
-      }
-    }
+    const int hb = i < nhw ? hw + i * wpt : hw;
+    const float* src = hb < nqh ? qg + ((size_t)tok * nqh + hb) * 512 : k + ((size_t)tok * nkvh + (hb - nqh)) * 256;
+    xin[i] = ld4_nt(src + off);
+  }
+#pragma unroll
+  for (int i = 0; i < HPW; i++) {
+    const int hb = hw + i * wpt;
+    if (i < nhw && hb >= nqh) vin[i] = ld4_nt(v + ((size_t)tok * nkvh + (hb - nqh)) * 256 + off);
   }
   const float4 qw = ld4(q_norm + off);
-  const float4 kw = nkvh ? ld4(k_norm + off) : qw;
-  // ---- rotary angles of the token: lane j < 32 evaluates pair j
-  float sn_j = 0.0f, cs_j = 1.0f;
-  if (p < 32) {
-    const int rp = rope3 ? rope3[tok * 3 + p % 3] : pos - (rdelta ? *rdelta : 0);
-    q27_sincos((float)rp * fr.f[p], &sn_j, &cs_j);
+  const float4 kw = ld4((nkvh ? k_norm : q_norm) + off);
+  // ---- rotary angles of the token, lane j < 32 evaluating pair j, from scalar loads and kernel arguments only
+  // (no wait on the vector loads above, so the sin/cos run while the head vectors are in flight)
+  const int j32 = p & 31;
+  int rp;
+  if (rope3) {
+    const int r0 = rope3[tok * 3], r1 = rope3[tok * 3 + 1], r2 = rope3[tok * 3 + 2];
+    const int m = j32 % 3;
+    rp = m == 0 ? r0 : m == 1 ? r1 : r2;
+  } else {
+    rp = pos - (rdelta ? *rdelta : 0);
   }
+  float fj = fr.f[0];  // fr.f[j32], selected from the argument registers
+#pragma unroll
+  for (int m = 1; m < 32; m++) {
+    float fm = fr.f[m];
+    asm("" : "+s"(fm));  // keeps the selects (no indexed load from the argument segment, which would wait behind the head loads)
+    fj = j32 == m ? fm : fj;
+  }
+  float sn_j, cs_j;
+  q27_sincos((float)rp * fj, &sn_j, &cs_j);
   float snc[4], csc[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
@@ -93,7 +107,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
 #pragma unroll
   for (int i = 0; i < HPW; i++) {
     if (i >= nhw) break;
-    const int hb = hb0 + i;
+    const int hb = hw + i * wpt;
     const bool isq = hb < nqh;
     const float x[4] = {xin[i].x, xin[i].y, xin[i].z, xin[i].w};
     const float sc = scale[i];
@@ -109,12 +123,12 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
     float partner[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) partner[c] = lane_xor<8>(buf[c]);
-    if (p < 8) {
+    // lanes 0..7: x0 * c - x1 * s; lanes 8..15: x0 * s + x1 * c (selects, no divergent branch)
 #pragma unroll
-      for (int c = 0; c < 4; c++) out[c] = buf[c] * csc[c] - partner[c] * snc[c];   // x0 * c - x1 * s
-    } else if (p < 16) {
-#pragma unroll
-      for (int c = 0; c < 4; c++) out[c] = partner[c] * snc[c] + buf[c] * csc[c];   // x0 * s + x1 * c
+    for (int c = 0; c < 4; c++) {
+      const float bc = buf[c] * csc[c], ps = partner[c] * snc[c];
+      const float r0 = bc - ps, r1 = ps + bc;
+      out[c] = p < 8 ? r0 : p < 16 ? r1 : buf[c];
     }
     if (isq) {
       st4(qn + ((size_t)tok * nqh + hb) * 256 + off, out[0], out[1], out[2], out[3]);

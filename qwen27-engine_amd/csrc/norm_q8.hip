@@ -81,15 +81,18 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 }
 
 // ---------------------------------------------------------------- flat q8_1 producers
-// A 256-thread workgroup covers kFlatU * 1024 consecutive values; in each 1024-value chunk thread t handles the 4
+// A 256-thread workgroup covers U * 1024 consecutive values; in each 1024-value chunk thread t handles the 4
 // values at 32 (t / 8) + 4 quad_of_lane(t % 8) (n % 32 == 0, so a q8 block is the 8 lanes of one group). All loads of a thread are
-// issued before any arithmetic so kFlatU * 16 (quantize) or 32 (swiglu) bytes per lane are in flight.
+// issued before any arithmetic so U * 16 (quantize) or U * 32 (swiglu) bytes per lane are in flight.
 #ifndef Q27H_FLAT_U
 #define Q27H_FLAT_U 2
 #endif
-constexpr int kFlatU = Q27H_FLAT_U;
+#ifndef Q27H_QUANT_U
+#define Q27H_QUANT_U 2
+#endif
+constexpr int kSwigluU = Q27H_FLAT_U, kQuantU = Q27H_QUANT_U;
 
-template <bool SWIGLU>
+template <bool SWIGLU, int kFlatU>
 __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                       int8_t* __restrict__ xq, float* __restrict__ xd,
                                                       float* __restrict__ xs, size_t n) {
@@ -258,11 +261,12 @@ int launch_flat(const char* fn, bool swiglu, const float* g, const float* u, int
   if (!g || !xq || !xd || (swiglu && !u)) return fail(Q27H_ERR_ARG, std::string(fn) + ": null pointer");
   if (!aligned16(g) || (swiglu && !aligned16(u)) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, std::string(fn) + ": inputs need 16-byte and xq 4-byte alignment");
-  const size_t blocks = (n + kFlatU * 1024 - 1) / (kFlatU * 1024);
+  const int U = swiglu ? kSwigluU : kQuantU;
+  const size_t blocks = (n + U * 1024 - 1) / (U * 1024);
   if (swiglu)
-    hipLaunchKernelGGL(flat_q8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
+    hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
   else
-    hipLaunchKernelGGL(flat_q8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
+    hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
   return check_launch(fn);
 }
 
