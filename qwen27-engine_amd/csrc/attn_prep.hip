@@ -14,6 +14,10 @@
 
 namespace q27h {
 namespace {
+#ifndef Q27H_NT_ATTN
+#define Q27H_NT_ATTN 1
+#endif
+constexpr bool kAttnNT = Q27H_NT_ATTN;  // nontemporal qn stores (measured in the prefill pass)
 
 struct RopeFreqs {
   float f[32];
@@ -131,7 +135,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
       out[c] = p < 8 ? r0 : p < 16 ? r1 : buf[c];
     }
     if (isq) {
-      st4(qn + ((size_t)tok * nqh + hb) * 256 + off, out[0], out[1], out[2], out[3]);
+      st4<kAttnNT>(qn + ((size_t)tok * nqh + hb) * 256 + off, out[0], out[1], out[2], out[3]);
       continue;
     }
     const int kh = hb - nqh;

@@ -24,6 +24,11 @@
 namespace q27h {
 namespace {
 
+#ifndef Q27H_NT_GDN
+#define Q27H_NT_GDN 1
+#endif
+constexpr bool kGdnNT = Q27H_NT_GDN;  // nontemporal stores of the prefill conv output
+
 __device__ __forceinline__ float conv4(float s0, float s1, float s2, float xn, const float (&w)[4]) {
   float sum = 0.0f;  // src/ops.cu:419-423: sum = 0; sum += s0 w0; sum += s1 w1; sum += s2 w2; sum += x w3
   sum += s0 * w[0];
@@ -145,7 +150,8 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
 #endif
       if (norm) l2_head_lanes(cur, eps);
       float* yr = y + (size_t)t * C + cb;
-      yr[0] = cur[0]; yr[32] = cur[1]; yr[64] = cur[2]; yr[96] = cur[3];
+#pragma unroll
+      for (int k = 0; k < 4; k++) st_f32<kGdnNT>(yr + 32 * k, cur[k]);
     }
 #pragma unroll
     for (int i = 0; i < CH; i++)

@@ -17,6 +17,30 @@ namespace {
 
 // ---------------------------------------------------------------- row engine
 enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2 };
+#ifndef Q27H_ROW_NT
+#define Q27H_ROW_NT 0
+#endif
+// Nontemporal stores per kernel (measured in the prefill pass)
+#ifndef Q27H_NT_ROW
+#define Q27H_NT_ROW 1
+#endif
+#ifndef Q27H_NT_SWIGLU
+#define Q27H_NT_SWIGLU 0
+#endif
+#ifndef Q27H_NT_QUANT
+#define Q27H_NT_QUANT 1
+#endif
+#ifndef Q27H_NT_GATED
+#define Q27H_NT_GATED 0
+#endif
+constexpr bool kRowNT = Q27H_NT_ROW, kSwigluNT = Q27H_NT_SWIGLU, kQuantNT = Q27H_NT_QUANT, kGatedNT = Q27H_NT_GATED;
+__device__ __forceinline__ float4 ld4_row(const float* p) {
+#if Q27H_ROW_NT
+  return ld4_nt(p);
+#else
+  return ld4(p);
+#endif
+}
 
 template <int MODE>
 __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x, const float* __restrict__ partial,
@@ -32,7 +56,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   float4 wv[5];
 #pragma unroll
   for (int k = 0; k < 5; k++) {
-    const float4 a = ld4(x + base + k * 1024);
+    const float4 a = ld4_row(x + base + k * 1024);
     v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
   }
 #pragma unroll
@@ -40,7 +64,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   if constexpr (MODE != kPlain) {
 #pragma unroll
     for (int k = 0; k < 5; k++) {
-      const float4 p = ld4(partial + base + k * 1024);
+      const float4 p = ld4_row(partial + base + k * 1024);
       const float pv[4] = {p.x, p.y, p.z, p.w};
       if constexpr (MODE == kAddPartial) {
 #pragma unroll
@@ -52,7 +76,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 #pragma unroll
         for (int c = 0; c < 4; c++) v[k][c] = v[k][c] + (bf16_round(pv[c]) + rv[c]);
       }
-      st4(x + base + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
+      st4<kRowNT>(x + base + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
     }
   }
   // per virtual thread: t = 0; t += v[k]^2 for k = 0..4 (src/ops.cu:96-98)
@@ -75,8 +99,8 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
     float y[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) y[c] = scale * v[k][c] * ww[c];
-    if (h) st4(h + base + k * 1024, y[0], y[1], y[2], y[3]);
-    q8_1_store4(y, xq, xd, xs, base + k * 1024);
+    if (h) st4<kRowNT>(h + base + k * 1024, y[0], y[1], y[2], y[3]);
+    q8_1_store4<kRowNT>(y, xq, xd, xs, base + k * 1024);
   }
 }
 
@@ -92,7 +116,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 #endif
 constexpr int kSwigluU = Q27H_FLAT_U, kQuantU = Q27H_QUANT_U;
 
-template <bool SWIGLU, int kFlatU>
+template <bool SWIGLU, int kFlatU, bool NT>
 __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                       int8_t* __restrict__ xq, float* __restrict__ xd,
                                                       float* __restrict__ xs, size_t n) {
@@ -106,6 +130,7 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
       if constexpr (SWIGLU) b[c] = ld4_nt(u + i0);
     }
   }
+  bool ok = true;  // every silu argument in the fast range (silu_fast_ok)
 #pragma unroll
   for (int c = 0; c < kFlatU; c++) {
     const size_t i0 = base + (size_t)c * 1024;
@@ -113,12 +138,29 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
     float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
     if constexpr (SWIGLU) {
       const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
-      float sg[4];
-      q27_silu_n(y, sg);
 #pragma unroll
-      for (int k = 0; k < 4; k++) y[k] = sg[k] * ub[k];
+      for (int k = 0; k < 4; k++) {
+        ok &= silu_fast_ok(y[k]);
+        y[k] = silu_fast(y[k]) * ub[k];
+      }
     }
-    q8_1_store4(y, xq, xd, xs, i0);
+    q8_1_store4<NT>(y, xq, xd, xs, i0);
+  }
+  // A wave with a silu argument outside the fast range (practically never) recomputes its values with the general
+  // silu and stores them again; in-range values are unchanged.
+  if constexpr (SWIGLU) {
+    if (__builtin_expect(__any(!ok), 0)) {
+#pragma unroll
+      for (int c = 0; c < kFlatU; c++) {
+        const size_t i0 = base + (size_t)c * 1024;
+        if (i0 >= n) break;
+        float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
+        const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) y[k] = q27_silu(y[k]) * ub[k];
+        q8_1_store4<NT>(y, xq, xd, xs, i0);
+      }
+    }
   }
 }
 
@@ -127,62 +169,49 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
 // of all of them issued first), a 256-thread workgroup 8 * kGatedH heads. The reference's 128-thread block_sum
 // (4 warps) becomes: per virtual warp (8 lanes) vwarp_sum4, then the second stage over the 4 warp sums with
 // zeros in lanes 4..31, i.e. (w0 + w2) + (w1 + w3) = lane xor 16, then lane xor 8.
-#ifndef Q27H_GATED_SILU_FIRST
-#define Q27H_GATED_SILU_FIRST 1
-#endif
-#ifndef Q27H_GATED_H
-#define Q27H_GATED_H 1
-#endif
-constexpr int kGatedH = Q27H_GATED_H;
-
+// silu(z) is evaluated on the fast range (silu_fast) without a branch, so it overlaps the norm's lane exchanges. A
+// wave with any z outside that range (zeros, subnormals, |z| > 60, inf, NaN; practically never) recomputes its
+// heads afterwards with the general silu and stores them again: the same addresses, the later store wins, and
+// the values of in-range lanes are unchanged.
+template <bool NT>
 __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __restrict__ o, const float* __restrict__ w,
                                                                const float* __restrict__ z, int8_t* __restrict__ xq,
                                                                float* __restrict__ xd, float eps, float* __restrict__ xs,
                                                                int heads) {
-  const int head0 = (blockIdx.x * 8 + (threadIdx.x >> 5)) * kGatedH;
-  if (head0 >= heads) return;  // whole 32-lane halves leave together
+  const int head = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (head >= heads) return;  // whole 32-lane halves leave together
   const int p = threadIdx.x & 31;
   const int off = 32 * (p >> 3) + block_offset(p);
-  const int nh = min(kGatedH, heads - head0);
-  float4 ov[kGatedH], zv[kGatedH];
-#pragma unroll
-  for (int k = 0; k < kGatedH; k++) {
-    if (k < nh) {
-      const size_t i0 = (size_t)(head0 + k) * 128 + off;
-      zv[k] = ld4_nt(z + i0);  // z first: silu(z) is computed first
-      ov[k] = ld4_nt(o + i0);
-    }
-  }
+  const size_t i0 = (size_t)head * 128 + off;
+  const float4 zv = ld4_nt(z + i0);  // z first: silu(z) is computed first
+  const float4 ov = ld4_nt(o + i0);
   const float4 wv = ld4(w + off);
   const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  const float v[4] = {ov.x, ov.y, ov.z, ov.w};
+  const float zz[4] = {zv.x, zv.y, zv.z, zv.w};
+  float gz[4];
+  bool ok = true;
 #pragma unroll
-  for (int k = 0; k < kGatedH; k++) {
-    if (k >= nh) break;
-    const size_t i0 = (size_t)(head0 + k) * 128 + off;
-    const float v[4] = {ov[k].x, ov[k].y, ov[k].z, ov[k].w};
-    const float zz[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
-#if Q27H_GATED_SILU_FIRST
-    float gz[4];  // silu(z) does not depend on the norm: issued first, it overlaps the reduction's lane exchanges
+  for (int c = 0; c < 4; c++) {
+    gz[c] = silu_fast(zz[c]);
+    ok &= silu_fast_ok(zz[c]);
+  }
+  float s[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) gz[c] = q27_silu(zz[c]);  // branch-free form: a branch here would end the overlap
-#endif
-    float s[4];
+  for (int c = 0; c < 4; c++) s[c] = v[c] * v[c];
+  float tsum = vwarp_sum4(s);
+  tsum = tsum + 0.0f;  // the reference adds the zero lanes 4..31 (xor 16, 8, 4 steps); x + 0 == x for x >= +0
+  tsum += lane_xor<16>(tsum);
+  tsum += lane_xor<8>(tsum);
+  const float scale = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
+  float y[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) s[c] = v[c] * v[c];
-    float tsum = vwarp_sum4(s);
-    tsum = tsum + 0.0f;  // the reference adds the zero lanes 4..31 (xor 16, 8, 4 steps); x + 0 == x for x >= +0
-    tsum += lane_xor<16>(tsum);
-    tsum += lane_xor<8>(tsum);
-    const float scale = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
-    float y[4];
-#if Q27H_GATED_SILU_FIRST
-#pragma unroll
-    for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * gz[c];
-#else
+  for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * gz[c];
+  q8_1_store4<NT>(y, xq, xd, xs, i0);
+  if (__builtin_expect(__any(!ok), 0)) {
 #pragma unroll
     for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * q27_silu(zz[c]);
-#endif
-    q8_1_store4(y, xq, xd, xs, i0);
+    q8_1_store4<NT>(y, xq, xd, xs, i0);
   }
 }
 
@@ -264,9 +293,11 @@ int launch_flat(const char* fn, bool swiglu, const float* g, const float* u, int
   const int U = swiglu ? kSwigluU : kQuantU;
   const size_t blocks = (n + U * 1024 - 1) / (U * 1024);
   if (swiglu)
-    hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
+    hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU, kSwigluNT>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd,
+                       xs, n);
   else
-    hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd, xs, n);
+    hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU, kQuantNT>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd,
+                       xs, n);
   return check_launch(fn);
 }
 
@@ -327,8 +358,8 @@ extern "C" int q27h_gated_rmsnorm_q8(const float* o, const float* w, const float
   if (!o || !w || !z || !xq || !xd) return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: null pointer");
   if (!aligned16(o) || !aligned16(w) || !aligned16(z) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: o, w, z need 16-byte and xq 4-byte alignment");
-  hipLaunchKernelGGL(gated_rmsnorm_q8_kernel, dim3((heads + 8 * kGatedH - 1) / (8 * kGatedH)), dim3(256), 0, stream_of(s), o, w, z, xq, xd, eps, xs,
-                     heads);
+  hipLaunchKernelGGL(gated_rmsnorm_q8_kernel<kGatedNT>, dim3((heads + 7) / 8), dim3(256), 0, stream_of(s), o, w, z, xq, xd,
+                     eps, xs, heads);
   return check_launch("gated_rmsnorm_q8");
 }
 

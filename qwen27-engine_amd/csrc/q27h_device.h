@@ -88,6 +88,44 @@ __device__ __forceinline__ float bf16_round(float f) {
 }
 __device__ __forceinline__ float bf16_to_f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
+// ---------------------------------------------------------------- global loads and stores
+__device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*)p; }
+// 16-byte streaming load (nontemporal hint: the data is read once), used where it measured faster: the SwiGLU
+// and quantizer inputs, the gated-norm inputs and the attention q/k/v.
+typedef float q27_v4f __attribute__((ext_vector_type(4)));
+#ifndef Q27H_NT
+#define Q27H_NT 1
+#endif
+__device__ __forceinline__ float4 ld4_nt(const float* p) {
+#if Q27H_NT
+  const q27_v4f v = __builtin_nontemporal_load((const q27_v4f*)p);
+  return make_float4(v.x, v.y, v.z, v.w);
+#else
+  return *(const float4*)p;
+#endif
+}
+// Stores. NT = nontemporal (streaming) hint, chosen per kernel from measurement: it pays where the written data
+// would otherwise still be draining from the caches when the next kernel runs.
+template <bool NT = false>
+__device__ __forceinline__ void st4(float* p, float a, float b, float c, float d) {
+  if constexpr (NT) {
+    const q27_v4f v = {a, b, c, d};
+    __builtin_nontemporal_store(v, (q27_v4f*)p);
+  } else {
+    *(float4*)p = make_float4(a, b, c, d);
+  }
+}
+template <bool NT = false>
+__device__ __forceinline__ void st_u32(void* p, uint32_t v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, (uint32_t*)p);
+  else *(uint32_t*)p = v;
+}
+template <bool NT = false>
+__device__ __forceinline__ void st_f32(float* p, float v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
 // ---------------------------------------------------------------- transcendental functions
 // exp: Cody-Waite reduction x = k ln2 + r, degree-7 Taylor polynomial of e^r (Horner, fma), ldexp.
 // Same operations and constants as the CPU checker (Muller, Elementary Functions, ch. 11).
@@ -166,6 +204,8 @@ __device__ __forceinline__ bool silu_fast_ok(float x) {
   const float ax = __builtin_fabsf(x);
   return ax >= 0x1p-60f && ax <= 60.0f;
 }
+// silu on the fast range only (2^-60 <= |x| <= 60, see silu_fast_ok); equal to q27_silu there.
+__device__ __forceinline__ float silu_fast(float x) { return div_in_range(x, 1.0f + q27_expf_core(-x)); }
 // N values at once, one branch for the lanes with an argument outside the fast range.
 template <int N>
 __device__ __forceinline__ void q27_silu_n(const float (&x)[N], float (&out)[N]) {
@@ -223,24 +263,36 @@ __device__ __forceinline__ void q27_sincos(float theta, float* s_out, float* c_o
 }
 
 // ---------------------------------------------------------------- q8 rounding
-// roundf(y / d) for |y| <= 127 d, d > 0 (the q8_1 rule of src/common.cuh:76), four values at a time. y * (1/d) is
-// within 2.3e-5 of the correctly rounded quotient, so away from the half-integers it rounds the same way and
-// rintf == roundf; a value within 2^-12 of a half-integer (or any value when 1/d is not finite) takes the IEEE
-// quotient. The rare exact path is one branch per four values.
+// amax / 127, correctly rounded, for amax >= 0: q0 = amax * RN(1/127), then one residual correction
+// r = amax - 127 q0 (exact in an fma), q0 + r * RN(1/127). The result equals the IEEE quotient for every finite
+// amax >= 0, subnormals included (checked exhaustively over all 2^31 non-negative finite floats on the host);
+// amax = +inf gives +inf and NaN stays NaN.
+constexpr float kInv127 = 1.0f / 127.0f;
+__device__ __forceinline__ float div127(float amax) {
+  const float q0 = amax * kInv127;
+  const float r = __builtin_fmaf(-127.0f, q0, amax);
+  const float q1 = __builtin_fmaf(r, kInv127, q0);
+  return amax == __builtin_huge_valf() ? amax : q1;
+}
+
+// roundf(y / d) for |y| <= 127 d (the q8_1 rule of src/common.cuh:76; q = 0 when d == 0), four values at a time.
+// For 2^-126 <= d <= 2^126, a = y * rcp(d) (v_rcp_f32, 1 ulp) is within 127 * 2^-22 < 3.1e-5 of the exact quotient,
+// so unless a lies within 2^-12 of a half-integer it rounds to the same integer as the correctly rounded quotient,
+// and rintf == roundf there. Values near a half-integer, NaN, d == 0 and d outside that range take the IEEE quotient:
+// one branch per four values, almost never taken.
 __device__ __forceinline__ void q8_round_div4(const float (&y)[4], float d, int (&q)[4]) {
-  const float rd = 1.0f / d;
-  bool slow = false;
+  const float rd = __builtin_amdgcn_rcpf(d);
+  bool slow = !(d >= 0x1p-126f && d <= 0x1p126f);
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     const float a = y[c] * rd;
-    const float fa = __builtin_fabsf(a);
-    const float fr = fa - __builtin_floorf(fa);
-    slow |= !(__builtin_fabsf(fr - 0.5f) > 2.44140625e-4f);
-    q[c] = (int)__builtin_rintf(a);
+    const float r = __builtin_rintf(a);
+    slow |= !(__builtin_fabsf(a - r) < 0.5f - 0x1p-12f);
+    q[c] = (int)r;
   }
   if (slow) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) q[c] = (int)__builtin_roundf(y[c] / d);
+    for (int c = 0; c < 4; c++) q[c] = d == 0.0f ? 0 : (int)__builtin_roundf(y[c] / d);
   }
 }
 
@@ -253,6 +305,7 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
 // as f32, and the optional per-16 sums of the unquantized values in the reference's butterfly order (xor 8, 4, 2, 1
 // over the 16 virtual lanes = lane xor 2, lane xor 1, then value pairs (0,2)(1,3), then (0,1)); the block's first
 // 16 values sit in lanes 0..3 of the group and the last 16 in lanes 4..7.
+template <bool NT = false>
 __device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restrict__ xq, float* __restrict__ xd,
                                             float* __restrict__ xs, size_t i0) {
   float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(y[0]), __builtin_fabsf(y[1])),
@@ -260,11 +313,11 @@ __device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restr
   amax = __builtin_fmaxf(amax, lane_xor<7>(amax));
   amax = __builtin_fmaxf(amax, lane_xor<2>(amax));
   amax = __builtin_fmaxf(amax, lane_xor<1>(amax));
-  const float d = amax / 127.0f;
-  int q[4] = {0, 0, 0, 0};
-  if (amax != 0.0f) q8_round_div4(y, d, q);
-  *(uint32_t*)(xq + i0) = pack4_i8(q[0], q[1], q[2], q[3]);
-  if ((i0 & 31) == 0) xd[i0 >> 5] = fp16_round(d);
+  const float d = div127(amax);
+  int q[4];
+  q8_round_div4(y, d, q);
+  st_u32<NT>(xq + i0, pack4_i8(q[0], q[1], q[2], q[3]));
+  if ((i0 & 31) == 0) st_f32<NT>(xd + (i0 >> 5), fp16_round(d));
   if (xs) {
     float u[4];
 #pragma unroll
@@ -272,7 +325,7 @@ __device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restr
 #pragma unroll
     for (int c = 0; c < 4; c++) u[c] = u[c] + lane_xor<1>(u[c]);
     const float tot = (u[0] + u[2]) + (u[1] + u[3]);
-    if ((i0 & 15) == 0) xs[i0 >> 4] = tot;
+    if ((i0 & 15) == 0) st_f32<NT>(xs + (i0 >> 4), tot);
   }
 }
 
@@ -302,22 +355,5 @@ __device__ __forceinline__ float red32_sum(const float* red) {
   v += lane_xor<1>(v);
   return v;
 }
-
-__device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*)p; }
-// 16-byte streaming load (nontemporal hint: the data is read once), used where it measured faster: the SwiGLU
-// and quantizer inputs, the gated-norm inputs and the attention q/k/v.
-typedef float q27_v4f __attribute__((ext_vector_type(4)));
-#ifndef Q27H_NT
-#define Q27H_NT 1
-#endif
-__device__ __forceinline__ float4 ld4_nt(const float* p) {
-#if Q27H_NT
-  const q27_v4f v = __builtin_nontemporal_load((const q27_v4f*)p);
-  return make_float4(v.x, v.y, v.z, v.w);
-#else
-  return *(const float4*)p;
-#endif
-}
-__device__ __forceinline__ void st4(float* p, float a, float b, float c, float d) { *(float4*)p = make_float4(a, b, c, d); }
 
 }  // namespace q27h
