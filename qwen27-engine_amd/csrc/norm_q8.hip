@@ -28,7 +28,7 @@ enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2 };
 #define Q27H_NT_SWIGLU 0
 #endif
 #ifndef Q27H_NT_QUANT
-#define Q27H_NT_QUANT 1
+#define Q27H_NT_QUANT 0
 #endif
 #ifndef Q27H_NT_GATED
 #define Q27H_NT_GATED 0
