@@ -30,6 +30,10 @@ C = 2 * KH * D + HV * D
 N_LAYER, N_CTX, VOCAB = 64, 180224, 248320
 EPS = 1e-6
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per swiglu_q8 launch at M = 2048, measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over the prefill
+# pass and scaled by the copy-kernel calibration (FETCH x 2.000, WRITE x 1.000): 139301 KiB and 47872 KiB
+# (profiles/hbm_traffic_prefill_pass.md). The counters cannot be read from inside this process.
+SWIGLU_TRAFFIC_BYTES = int((139301 * 2.0 + 47872 * 1.0) * 1024)
 
 
 def is_attn(il):
@@ -514,13 +518,26 @@ def main():
     acc = {}
     for _ in range(max(1, min(3, args.steps))):
         P.run_events(acc)
+    # An event pair around every launch adds a fixed cost per launch (the kernel waits behind the event marker).
+    # It is estimated as (sum of the per-launch event times - the pass time without events) / launches and
+    # subtracted in "net_us"; the rocprof kernel durations in profiles/ are the direct measurement.
+    npass = max(1, min(3, args.steps))
+    ev_total_us = sum(ms for ms, _, _ in acc.values()) * 1e3 / npass
+    n_launch = sum(cnt for _, cnt, _ in acc.values()) // npass
+    ev_overhead_us = max(0.0, (ev_total_us - ms_per_step * 1e3) / n_launch)
+    log(f"event-pair overhead: {ev_overhead_us:.2f} us per launch")
     per_op = {}
     for name, (ms, cnt, b) in acc.items():
         us = ms * 1e3 / cnt
+        net = max(us - ev_overhead_us, 1e-3)
         gbs = (b / cnt) / (us * 1e-6) / 1e9
+        gbs_net = (b / cnt) / (net * 1e-6) / 1e9
         per_op[name] = {"us": round(us, 2), "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
-                        "bytes": b // cnt, "launches_per_step": cnt // max(1, min(3, args.steps))}
-        log(f"  {name:18s} {us:9.2f} us  {gbs:8.1f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+                        "net_us": round(net, 2), "net_GBps": round(gbs_net, 1),
+                        "net_hbm_frac": round(gbs_net / HBM_PEAK_GBS, 3),
+                        "bytes": b // cnt, "launches_per_step": cnt // npass}
+        log(f"  {name:18s} {us:9.2f} us  {gbs:8.1f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s); "
+            f"net {net:7.2f} us ({gbs_net / HBM_PEAK_GBS:.1%})")
     # ---- roofline of the dominant kernel (swiglu_q8 at M = 2048): back-to-back launches between two HIP events
     # on the stream the kernel runs on (torch's current stream, which the launchers use)
     # Three input sets are cycled (3 x 285 MB of g, u) so no launch finds its inputs in the 256 MB MALL.
@@ -540,7 +557,7 @@ def main():
     sw_gbs = sw_bytes / (sw_us * 1e-6) / 1e9
     log(f"swiglu_q8 back-to-back: {sw_us:.2f} us per launch, {sw_gbs:.0f} GB/s")
     roofline = {"bound": "hbm", "achieved": round(sw_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(sw_gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "swiglu_q8 (flat_q8_kernel<true>)",
+                "frac": round(sw_gbs / HBM_PEAK_GBS, 4), "traffic": SWIGLU_TRAFFIC_BYTES, "kernel": "swiglu_q8 (flat_q8_kernel<true>)",
                 "bytes_per_launch": sw_bytes, "avg_launch_us": round(sw_us, 2),
                 "note": "2048 x 17408 values, 9.375 B each (g, u f32 in; xq int8, xd f32 per 32, xs f32 per 16 out)"}
     # ---- practical copy ceiling of this device (torch device-to-device copy of 512 MiB, read + write bytes)
@@ -628,6 +645,7 @@ def main():
         "us_per_2048_batch": round(ms_per_step * 1e3, 1),
         "decode_us_per_step": round(decode_us, 1),
         "per_op": per_op,
+        "per_op_event_overhead_us": round(ev_overhead_us, 2),
         "decode_per_op": decode_ops,
         "cfg1_rmsnorm_q8_row": cfg1,
         "gathers_cfg4": gathers,
