@@ -133,6 +133,22 @@ int q27h_get_rows_q6_k(const uint8_t* table, int64_t row_bytes, const int* ids, 
 int q27h_get_rows_q8_0(const uint8_t* table, int64_t row_bytes, const int* ids, int T, float* y, int n, q27h_stream_t s,
                        const float* img);
 
+/* ---------------------------------------------------------------- decode GEMV over quantized weights
+ * Weight types are ggml type ids (src/gguf.h:12-14): 12 Q4_K, 14 Q6_K, 21 IQ3_S, 23 IQ4_XS. A matrix of N rows
+ * (outputs, N % 8 == 0) and K columns (K % 256 == 0) lives in one caller-owned device buffer in the tile layout
+ * of the reference's QMat (src/qmat.h:1-8).
+ * q27h_qmat_bytes (src/qmat.h:31): bytes of that buffer (0 for an unsupported type or shape). */
+size_t q27h_qmat_bytes(int type, int N, int K);
+/* Repack (the device half of qmat_upload, src/qmat.h:34, src/qgemv.cu:227-260): raw = N GGUF rows already in device
+ * memory ([N][K/256] blocks), buf = q27h_qmat_bytes() bytes, 256-byte aligned. Byte moves only. */
+int q27h_qmat_repack(int type, int N, int K, const void* raw, void* buf, q27h_stream_t s);
+/* qgemv (src/qmat.h:44-46, src/qgemv.cu:785-801): y[c][n] = sum_k W[n][k] x[c][k] for c < ncols (1..4; the reference
+ * takes 1, 2 or 4), x as q8_1 activations xq [ncols][K] (16-byte aligned), xd [ncols][K/32]. */
+int q27h_qgemv(int type, int N, int K, const void* buf, const int8_t* xq, const float* xd, float* y, int ncols,
+               q27h_stream_t s);
+/* Waves that share one 8-row tile in q27h_qgemv (1, 2 or 4): part of the summation order, a function of N only. */
+int q27h_qgemv_waves(int N, int K);
+
 #ifdef __cplusplus
 }
 #endif

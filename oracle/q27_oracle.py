@@ -55,6 +55,9 @@ _SIGS = {
     "q27o_get_rows_q6_k": (None, [_p, _i64, _p, _i, _p, _i, _p]),
     "q27o_get_rows_q8_0": (None, [_p, _i64, _p, _i, _p, _i, _p]),
     "q27o_iq2s_grid": (C.POINTER(C.c_uint64), []),
+    "q27o_qgemv_block_bytes": (_i, [_i]),
+    "q27o_qgemv_waves": (_i, [_i, _i]),
+    "q27o_qgemv": (_i, [_i, _p, _i, _i, _p, _p, _p, _i]),
 }
 
 _lib = None
@@ -300,3 +303,18 @@ def get_rows(kind, table, row_bytes, ids, n, img=None):
 def iq2s_grid() -> np.ndarray:
     p = lib().q27o_iq2s_grid()
     return np.ctypeslib.as_array(p, shape=(1024,)).copy()
+
+
+def qgemv(type_, raw, N, K, xq, xd, ncols):
+    """Decode GEMV over raw GGUF rows (q27_oracle_qgemv.c): returns y [ncols][N] (f32)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    xd = _f32(xd)
+    y = np.zeros(ncols * N, np.float32)
+    if lib().q27o_qgemv(type_, _ptr(raw), N, K, _ptr(xq), _ptr(xd), _ptr(y), ncols) != 0:
+        raise ValueError("q27o_qgemv: bad type or shape")
+    return y.reshape(ncols, N)
+
+
+def qgemv_waves(N, K):
+    return int(lib().q27o_qgemv_waves(N, K))

@@ -46,10 +46,14 @@ SIGNATURES = {
     "q27h_get_rows_q4_k": [_p, _i64, _p, _i, _p, _i, _p, _p],
     "q27h_get_rows_q6_k": [_p, _i64, _p, _i, _p, _i, _p, _p],
     "q27h_get_rows_q8_0": [_p, _i64, _p, _i, _p, _i, _p, _p],
+    "q27h_qmat_bytes": [_i, _i, _i],
+    "q27h_qmat_repack": [_i, _i, _i, _p, _p, _p],
+    "q27h_qgemv": [_i, _i, _i, _p, _p, _p, _p, _i, _p],
+    "q27h_qgemv_waves": [_i, _i],
     "q27h_last_error": [],
     "q27h_abi_version": [],
 }
-_RESTYPE = {"q27h_kv_cache_bytes": _sz, "q27h_last_error": C.c_char_p}
+_RESTYPE = {"q27h_kv_cache_bytes": _sz, "q27h_qmat_bytes": _sz, "q27h_last_error": C.c_char_p}
 
 _lib = None
 

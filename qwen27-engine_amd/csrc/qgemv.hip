@@ -1,0 +1,505 @@
+// Decode GEMV over quantized weights (the consumer of the q8_1 activations): y[c][n] = sum_k W[n][k] x[c][k] for
+// 1..4 activation columns, W in GGUF block types Q4_K, Q6_K, IQ3_S and IQ4_XS repacked into the tile layout of the
+// reference's QMat (src/qmat.h:1-8): 8 rows per tile; chunk = (tile, 256-weight block b, 32-weight sub-block s),
+// chunk index (tile * nb + b) * 8 + s; every field of the block struct goes to its own array ordered by chunk, then
+// by row inside the tile; the super-block scales go to an array ordered by (tile, block), then row. The repack only
+// moves bytes, so every weight decodes to the value it has in the GGUF block.
+//
+// Kernel (gfx950): a 256-thread workgroup = 4 waves. W waves (1, 2 or 4, a function of the shape only) share one
+// tile; lane l = 8 lb + s of wave w takes sub-block s of the blocks b = 8 w + lb, + 8 W, ... and keeps the 8 rows x
+// ncols partial sums in registers, so one load of its 32 activations per column serves 8 rows. Integer dot products
+// per sub-block use v_dot4_i32_i8 (exact); the float contribution of each sub-block is the reference's expression of
+// that type (src/qgemv.cu:369-560). The 64 lane sums are added as an xor butterfly in which each exchange level sends
+// half of the remaining values (lane xor 32 .. 1), and the W wave sums go through LDS and are added in wave order.
+// The same summation order is restated by the CPU checker, so results are bit-identical to it.
+#include "q27h_device.h"
+#include "q27h_internal.h"
+
+namespace q27h {
+namespace {
+
+constexpr int kQ4K = 12, kQ6K = 14, kIQ3S = 21, kIQ4XS = 23;
+
+__device__ const uint32_t kIQ3SGrid[512] = {
+#include "iq3s_grid.inc"
+};
+__device__ const int8_t kIQ4NL[16] = {
+#include "iq4nl_values.inc"
+};
+
+// Per-type field widths (bytes per chunk, 8 rows), scale bytes per (tile, block), GGUF block bytes.
+struct Fmt {
+  int nf;
+  int w[4];
+  int dw;
+  int bb;
+};
+__host__ __device__ constexpr Fmt fmt_of(int type) {
+  return type == kQ4K    ? Fmt{2, {128, 16, 0, 0}, 32, 144}
+         : type == kQ6K  ? Fmt{3, {128, 64, 16, 0}, 16, 210}
+         : type == kIQ3S ? Fmt{4, {64, 32, 8, 4}, 16, 110}
+         : type == kIQ4XS ? Fmt{2, {128, 8, 0, 0}, 16, 136}
+                          : Fmt{0, {0, 0, 0, 0}, 0, 0};
+}
+inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+struct Mat {
+  const uint8_t* f[4];
+  const uint8_t* d;
+  int N, nb, ntiles;
+};
+
+// Field offsets inside the QMat buffer: the fields in order, then the scales, each 256-byte aligned.
+size_t layout(int type, int N, int K, size_t off[5]) {
+  const Fmt F = fmt_of(type);
+  const size_t ntb = (size_t)(N / 8) * (K / 256);
+  size_t o = 0;
+  for (int i = 0; i < 4; i++) {
+    off[i] = o;
+    if (i < F.nf) o += align256(ntb * 8 * F.w[i]);
+  }
+  off[4] = o;
+  return o + align256(ntb * F.dw);
+}
+
+// ---------------------------------------------------------------- repack (one thread per chunk)
+template <int TYPE>
+__global__ void repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ f0, uint8_t* __restrict__ f1,
+                              uint8_t* __restrict__ f2, uint8_t* __restrict__ f3, uint8_t* __restrict__ dd, int nb,
+                              size_t nchunks) {
+  const size_t chunk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (chunk >= nchunks) return;
+  constexpr Fmt F = fmt_of(TYPE);
+  const int s = (int)(chunk & 7);
+  const size_t tb = chunk >> 3;
+  const int b = (int)(tb % nb);
+  const size_t tile = tb / nb;
+  uint8_t* o0 = f0 + chunk * F.w[0];
+  uint8_t* o1 = f1 + chunk * F.w[1];
+  uint8_t* o2 = F.nf > 2 ? f2 + chunk * F.w[2] : nullptr;
+  uint32_t nib = 0;
+  for (int r = 0; r < 8; r++) {
+    const uint8_t* src = raw + ((tile * 8 + r) * nb + b) * F.bb;
+    uint8_t* od = dd + tb * F.dw;
+    if constexpr (TYPE == kQ4K) {  // d, dmin, scales[12], qs[128]
+      const uint8_t* qs = src + 16 + 32 * (s / 2);
+      const int sh = 4 * (s & 1);
+      for (int k = 0; k < 16; k++)  // byte k: weight k (low nibble), weight k + 16 (high nibble)
+        o0[16 * r + k] = (uint8_t)(((qs[k] >> sh) & 0xF) | (((qs[k + 16] >> sh) & 0xF) << 4));
+      const uint8_t* sc = src + 4;
+      int scv, mv;
+      if (s < 4) {
+        scv = sc[s] & 63;
+        mv = sc[s + 4] & 63;
+      } else {
+        scv = (sc[s + 4] & 0xF) | ((sc[s - 4] >> 6) << 4);
+        mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
+      }
+      o1[2 * r] = (uint8_t)scv;
+      o1[2 * r + 1] = (uint8_t)mv;
+      if (s == 0)
+        for (int k = 0; k < 4; k++) od[4 * r + k] = src[k];
+    } else if constexpr (TYPE == kQ6K) {  // ql[128], qh[64], scales[16], d
+      const int n = s / 4, j = s % 4;
+      uint8_t q[32];
+      for (int l = 0; l < 32; l++) {
+        const uint8_t lo = src[64 * n + 32 * (j & 1) + l];
+        const uint8_t hi = src[128 + 32 * n + l];
+        q[l] = (uint8_t)(((j < 2 ? lo : lo >> 4) & 0xF) | (((hi >> (2 * j)) & 3) << 4));
+      }
+      for (int k = 0; k < 16; k++) o0[16 * r + k] = (uint8_t)((q[k] & 0xF) | ((q[k + 16] & 0xF) << 4));
+      for (int h = 0; h < 2; h++)  // word h (weights 16 h ..): byte k holds the high bits of weights 16 h + k + 4 i
+        for (int k = 0; k < 4; k++) {
+          uint8_t v = 0;
+          for (int i = 0; i < 4; i++) v |= (uint8_t)(((q[16 * h + k + 4 * i] >> 4) & 3) << (2 * i));
+          o1[8 * r + 4 * h + k] = v;
+        }
+      o2[2 * r] = src[192 + 8 * n + 2 * j];
+      o2[2 * r + 1] = src[192 + 8 * n + 2 * j + 1];
+      if (s == 0) {
+        od[2 * r] = src[208];
+        od[2 * r + 1] = src[209];
+      }
+    } else if constexpr (TYPE == kIQ3S) {  // d, qs[64], qh[8], signs[32], scales[4]
+      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
+      for (int k = 0; k < 4; k++) o1[4 * r + k] = src[74 + 4 * s + k];
+      o2[r] = src[66 + s];
+      nib |= (uint32_t)((src[106 + s / 2] >> (4 * (s & 1))) & 0xF) << (4 * r);
+      if (s == 0) {
+        od[2 * r] = src[0];
+        od[2 * r + 1] = src[1];
+      }
+    } else if constexpr (TYPE == kIQ4XS) {  // d, scales_h (u16), scales_l[4], qs[128]
+      for (int k = 0; k < 16; k++) o0[16 * r + k] = src[8 + 16 * s + k];
+      const int sh = src[2] | (src[3] << 8);
+      const int l = ((src[4 + s / 2] >> (4 * (s & 1))) & 0xF) | (((sh >> (2 * s)) & 3) << 4);
+      o1[r] = (uint8_t)(int8_t)(l - 32);
+      if (s == 0) {
+        od[2 * r] = src[0];
+        od[2 * r + 1] = src[1];
+      }
+    }
+  }
+  if constexpr (TYPE == kIQ3S) *(uint32_t*)(f3 + chunk * 4) = nib;
+}
+
+// ---------------------------------------------------------------- decode of one chunk
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+__device__ __forceinline__ float half_lo(uint32_t w) { return h2f_bits((uint16_t)(w & 0xFFFF)); }
+__device__ __forceinline__ float half_hi(uint32_t w) { return h2f_bits((uint16_t)(w >> 16)); }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <int N>
+__device__ __forceinline__ void ld16(uint32_t* w, const uint8_t* p) {  // N x 16 bytes, streaming (read once)
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p + i);
+    w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+  }
+}
+
+// Bytes of g negated where the matching bit of the 4-bit mask is set (g's bytes are magnitudes 1..127, so
+// two's complement per byte, (b ^ 0xFF) + 1, never carries into the next byte).
+__device__ __forceinline__ int signed_bytes(uint32_t g, uint32_t nib4) {
+  const uint32_t ones = ((nib4 & 1u) | ((nib4 & 2u) << 7) | ((nib4 & 4u) << 14) | ((nib4 & 8u) << 21));
+  return (int)((g ^ (ones * 0xFFu)) + ones);
+}
+
+// IQ4_XS levels of 4 nibbles (one per byte, values 0..15) via two byte permutes of the 16-entry table.
+__device__ __forceinline__ int iq4_levels(uint32_t nib, const uint32_t (&t)[4]) {
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel);  // entries 0..7
+  const uint32_t hi = __builtin_amdgcn_perm(t[3], t[2], sel);  // entries 8..15
+  const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+  return (int)((hi & m) | (lo & ~m));
+}
+
+template <int TYPE>
+struct Chunk {
+  static constexpr Fmt F = fmt_of(TYPE);
+  static constexpr int nw = (F.w[0] + F.w[1] + F.w[2] + F.w[3]) / 4 + F.dw / 4;
+  uint32_t w[nw];
+};
+
+template <int TYPE>
+__device__ __forceinline__ void load_chunk(Chunk<TYPE>& c, const Mat& m, size_t tb, int s) {
+  const size_t ch = tb * 8 + s;
+  if constexpr (TYPE == kQ4K) {
+    ld16<8>(c.w, m.f[0] + ch * 128);
+    ld16<1>(c.w + 32, m.f[1] + ch * 16);
+    ld16<2>(c.w + 36, m.d + tb * 32);
+  } else if constexpr (TYPE == kQ6K) {
+    ld16<8>(c.w, m.f[0] + ch * 128);
+    ld16<4>(c.w + 32, m.f[1] + ch * 64);
+    ld16<1>(c.w + 48, m.f[2] + ch * 16);
+    ld16<1>(c.w + 52, m.d + tb * 16);
+  } else if constexpr (TYPE == kIQ3S) {
+    ld16<4>(c.w, m.f[0] + ch * 64);
+    ld16<2>(c.w + 16, m.f[1] + ch * 32);
+    const u32x2 h = __builtin_nontemporal_load((const u32x2*)(m.f[2] + ch * 8));
+    c.w[24] = h.x; c.w[25] = h.y;
+    c.w[26] = __builtin_nontemporal_load((const uint32_t*)(m.f[3] + ch * 4));
+    ld16<1>(c.w + 27, m.d + tb * 16);
+  } else if constexpr (TYPE == kIQ4XS) {
+    ld16<8>(c.w, m.f[0] + ch * 128);
+    const u32x2 l = __builtin_nontemporal_load((const u32x2*)(m.f[1] + ch * 8));
+    c.w[32] = l.x; c.w[33] = l.y;
+    ld16<1>(c.w + 34, m.d + tb * 16);
+  }
+}
+
+// acc[r * NC + c] += t(row r, column c) for one chunk; u[c] = the 32 int8 activations of column c, dy[c] its scale.
+template <int TYPE, int NC>
+__device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[NC][8], const float (&dy)[NC],
+                                          const uint32_t* __restrict__ lut, const uint32_t (&kv)[4],
+                                          float (&acc)[8 * NC]) {
+  const uint32_t* w = ch.w;
+  if constexpr (TYPE == kQ4K) {
+    int s8[NC];  // sums of the activations: the min term (dmin * m) multiplies them
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      int t = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) t = dot4(u[c][k], 0x01010101, t);
+      s8[c] = t;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      int sumi[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) sumi[c] = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int lo = (int)(w[4 * r + j] & 0x0F0F0F0Fu), hi = (int)((w[4 * r + j] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+        for (int c = 0; c < NC; c++) sumi[c] = dot4(hi, u[c][j + 4], dot4(lo, u[c][j], sumi[c]));
+      }
+      const uint32_t sm = w[32 + r / 2] >> (16 * (r & 1));
+      const int sc = (int)(sm & 0xFF), mn = (int)((sm >> 8) & 0xFF);
+      const float d = half_lo(w[36 + r]), dmin = half_hi(w[36 + r]);
+#pragma unroll
+      for (int c = 0; c < NC; c++)
+        acc[r * NC + c] += d * (dy[c] * (float)(sumi[c] * sc)) - dmin * (dy[c] * (float)(s8[c] * mn));
+    }
+  } else if constexpr (TYPE == kQ6K) {
+    int s8a[NC], s8b[NC];  // activation sums of the two 16-weight halves (the -32 offset of the quants)
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      int ta = 0, tb = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        ta = dot4(u[c][k], 0x01010101, ta);
+        tb = dot4(u[c][k + 4], 0x01010101, tb);
+      }
+      s8a[c] = ta;
+      s8b[c] = tb;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      int sa[NC], sb[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) sa[c] = sb[c] = 0;
+      const uint32_t h0 = w[32 + 2 * r], h1 = w[33 + 2 * r];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t l = w[4 * r + i];
+        const int qa = (int)((l & 0x0F0F0F0Fu) | (((h0 >> (2 * i)) & 0x03030303u) << 4));
+        const int qb = (int)(((l >> 4) & 0x0F0F0F0Fu) | (((h1 >> (2 * i)) & 0x03030303u) << 4));
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          sa[c] = dot4(qa, u[c][i], sa[c]);
+          sb[c] = dot4(qb, u[c][4 + i], sb[c]);
+        }
+      }
+      const uint32_t g = w[48 + r / 2] >> (16 * (r & 1));
+      const int sc0 = (int)(int8_t)(g & 0xFF), sc1 = (int)(int8_t)((g >> 8) & 0xFF);
+      const float d = (r & 1) ? half_hi(w[52 + r / 2]) : half_lo(w[52 + r / 2]);
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const int si = (sa[c] - 32 * s8a[c]) * sc0 + (sb[c] - 32 * s8b[c]) * sc1;
+        acc[r * NC + c] += d * (dy[c] * (float)si);
+      }
+    }
+  } else if constexpr (TYPE == kIQ3S) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const uint32_t qh = (w[24 + r / 4] >> (8 * (r & 3))) & 0xFF;
+      const uint32_t sg = w[16 + r];
+      int sumi[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) sumi[c] = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const uint32_t idx = ((w[2 * r + k / 4] >> (8 * (k & 3))) & 0xFF) | ((qh << (8 - k)) & 0x100);
+        const int g = signed_bytes(lut[idx], (sg >> (4 * k)) & 0xF);
+#pragma unroll
+        for (int c = 0; c < NC; c++) sumi[c] = dot4(g, u[c][k], sumi[c]);
+      }
+      const int mul = 1 + 2 * (int)((w[26] >> (4 * r)) & 0xF);
+      const float d = (r & 1) ? half_hi(w[27 + r / 2]) : half_lo(w[27 + r / 2]);
+#pragma unroll
+      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)(sumi[c] * mul);
+    }
+  } else if constexpr (TYPE == kIQ4XS) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      int sumi[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) sumi[c] = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t q = w[4 * r + j];
+        const int lo = iq4_levels(q & 0x0F0F0F0Fu, kv), hi = iq4_levels((q >> 4) & 0x0F0F0F0Fu, kv);
+#pragma unroll
+        for (int c = 0; c < NC; c++) sumi[c] = dot4(hi, u[c][j + 4], dot4(lo, u[c][j], sumi[c]));
+      }
+      const int ls = (int)(int8_t)((w[32 + r / 4] >> (8 * (r & 3))) & 0xFF);
+      const float d = (r & 1) ? half_hi(w[34 + r / 2]) : half_lo(w[34 + r / 2]);
+#pragma unroll
+      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)(sumi[c] * ls);
+    }
+  }
+}
+
+// Value of lane (lane ^ O) over the whole wave.
+template <int O>
+__device__ __forceinline__ float xchg(float v) {
+  if constexpr (O == 32) return lane_xor32(v);
+  else return lane_xor<O>(v);
+}
+// One butterfly level: lanes with bit O set keep the upper half of the live values, the others the lower half;
+// each adds the partner's copy of the same values.
+template <int O, int V>
+__device__ __forceinline__ void reduce_level(float (&a)[V], int& cur, int lane) {
+  if (cur > 1) {
+    const int h = cur / 2;
+    const bool up = (lane & O) != 0;
+#pragma unroll
+    for (int i = 0; i < V / 2; i++) {
+      if (i < h) {
+        const float send = up ? a[i] : a[i + h];
+        const float keep = up ? a[i + h] : a[i];
+        a[i] = keep + xchg<O>(send);
+      }
+    }
+    cur = h;
+  } else {
+    a[0] += xchg<O>(a[0]);
+  }
+}
+
+constexpr int waves_per_tile(int N) {
+  return N / 8 >= 1536 ? 1 : N / 8 >= 768 ? 2 : 4;
+}
+
+template <int TYPE, int NC>
+__global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                    float* __restrict__ y, int K, int W) {
+  __shared__ uint32_t lut[TYPE == kIQ3S ? 512 : 1];
+  __shared__ float part[4][8 * NC];
+  if constexpr (TYPE == kIQ3S) {
+    for (int i = threadIdx.x; i < 512; i += 256) lut[i] = kIQ3SGrid[i];
+  }
+  uint32_t kv[4] = {0, 0, 0, 0};
+  if constexpr (TYPE == kIQ4XS) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      kv[i] = (uint32_t)(uint8_t)kIQ4NL[4 * i] | ((uint32_t)(uint8_t)kIQ4NL[4 * i + 1] << 8) |
+              ((uint32_t)(uint8_t)kIQ4NL[4 * i + 2] << 16) | ((uint32_t)(uint8_t)kIQ4NL[4 * i + 3] << 24);
+  }
+  if constexpr (TYPE == kIQ3S) __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tile = blockIdx.x * (4 / W) + wave / W;
+  const int wv = wave % W;
+  const int lb = lane >> 3, s = lane & 7;
+  const bool live = tile < m.ntiles;  // uniform per wave
+  float acc[8 * NC];
+#pragma unroll
+  for (int i = 0; i < 8 * NC; i++) acc[i] = 0.0f;
+  if (live) {
+    for (int b = 8 * wv + lb; b < m.nb; b += 8 * W) {
+      Chunk<TYPE> ch;
+      load_chunk<TYPE>(ch, m, (size_t)tile * m.nb + b, s);
+      int u[NC][8];
+      float dy[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const int4* xp = (const int4*)(xq + (size_t)c * K + (size_t)b * 256 + s * 32);
+        const int4 a0 = xp[0], a1 = xp[1];
+        u[c][0] = a0.x; u[c][1] = a0.y; u[c][2] = a0.z; u[c][3] = a0.w;
+        u[c][4] = a1.x; u[c][5] = a1.y; u[c][6] = a1.z; u[c][7] = a1.w;
+        dy[c] = xd[(size_t)c * (K / 32) + b * 8 + s];
+      }
+      dot_chunk<TYPE, NC>(ch, u, dy, lut, kv, acc);
+    }
+  }
+  // 64-lane butterfly; afterwards lane l holds value index l >> (6 - log2(8 NC)) (copies in the lower lane bits)
+  constexpr int V = 8 * NC;
+  int cur = V;
+  reduce_level<32>(acc, cur, lane);
+  reduce_level<16>(acc, cur, lane);
+  reduce_level<8>(acc, cur, lane);
+  reduce_level<4>(acc, cur, lane);
+  reduce_level<2>(acc, cur, lane);
+  reduce_level<1>(acc, cur, lane);
+  constexpr int shift = V == 8 ? 3 : V == 16 ? 2 : V == 32 ? 1 : 0;  // NC = 3 (V = 24) is handled on the host
+  const int idx = lane >> shift;
+  const bool writer = (lane & ((1 << shift) - 1)) == 0;
+  if (W == 1) {
+    if (live && writer) y[(size_t)(idx % NC) * m.N + tile * 8 + idx / NC] = acc[0];
+    return;
+  }
+  if (writer) part[wave][idx] = acc[0];
+  __syncthreads();
+  if (live && wv == 0 && writer) {
+    float t = part[wave][idx];
+    for (int k = 1; k < W; k++) t = t + part[wave + k][idx];
+    y[(size_t)(idx % NC) * m.N + tile * 8 + idx / NC] = t;
+  }
+}
+
+int check_type(int type) {
+  if (fmt_of(type).nf == 0) return fail(Q27H_ERR_UNSUPPORTED, "qgemv: weight type " + std::to_string(type) + " not supported");
+  return Q27H_OK;
+}
+
+template <int TYPE, int NC>
+void launch_gemv(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, hipStream_t s) {
+  const int W = waves_per_tile(m.N);
+  const int grid = (m.ntiles * W + 3) / 4;
+  hipLaunchKernelGGL((qgemv_kernel<TYPE, NC>), dim3(grid), dim3(256), 0, s, m, xq, xd, y, K, W);
+}
+
+template <int TYPE>
+void launch_nc(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, int nc, hipStream_t s) {
+  if (nc == 1) launch_gemv<TYPE, 1>(m, xq, xd, y, K, s);
+  else if (nc == 2) launch_gemv<TYPE, 2>(m, xq, xd, y, K, s);
+  else launch_gemv<TYPE, 4>(m, xq, xd, y, K, s);
+}
+
+}  // namespace
+}  // namespace q27h
+
+using namespace q27h;
+
+extern "C" size_t q27h_qmat_bytes(int type, int N, int K) {
+  if (fmt_of(type).nf == 0 || N <= 0 || K <= 0 || N % 8 || K % 256) return 0;
+  size_t off[5];
+  return layout(type, N, K, off);
+}
+
+extern "C" int q27h_qgemv_waves(int N, int K) {
+  (void)K;
+  return waves_per_tile(N);
+}
+
+extern "C" int q27h_qmat_repack(int type, int N, int K, const void* raw, void* buf, q27h_stream_t s) {
+  if (int e = check_type(type)) return e;
+  if (N <= 0 || K <= 0 || N % 8 || K % 256) return fail(Q27H_ERR_SHAPE, "qmat_repack: N % 8 and K % 256 must be 0");
+  if (!raw || !buf) return fail(Q27H_ERR_ARG, "qmat_repack: null pointer");
+  if (((uintptr_t)buf & 255u) != 0) return fail(Q27H_ERR_ARG, "qmat_repack: buf needs 256-byte alignment");
+  size_t off[5];
+  layout(type, N, K, off);
+  uint8_t* b = (uint8_t*)buf;
+  const size_t nchunks = (size_t)(N / 8) * (K / 256) * 8;
+  const dim3 grid((unsigned)((nchunks + 255) / 256));
+  const uint8_t* r = (const uint8_t*)raw;
+  const int nb = K / 256;
+  switch (type) {
+    case kQ4K: hipLaunchKernelGGL(repack_kernel<kQ4K>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
+    case kQ6K: hipLaunchKernelGGL(repack_kernel<kQ6K>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
+    case kIQ3S: hipLaunchKernelGGL(repack_kernel<kIQ3S>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
+    default: hipLaunchKernelGGL(repack_kernel<kIQ4XS>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
+  }
+  return check_launch("qmat_repack");
+}
+
+extern "C" int q27h_qgemv(int type, int N, int K, const void* buf, const int8_t* xq, const float* xd, float* y, int ncols,
+                          q27h_stream_t s) {
+  if (int e = check_type(type)) return e;
+  if (N <= 0 || K <= 0 || N % 8 || K % 256) return fail(Q27H_ERR_SHAPE, "qgemv: N % 8 and K % 256 must be 0");
+  if (ncols < 1 || ncols > 4) return fail(Q27H_ERR_SHAPE, "qgemv: ncols must be 1..4");
+  if (!buf || !xq || !xd || !y) return fail(Q27H_ERR_ARG, "qgemv: null pointer");
+  if (((uintptr_t)buf & 255u) != 0 || !aligned16(xq)) return fail(Q27H_ERR_ARG, "qgemv: buf needs 256-byte and xq 16-byte alignment");
+  size_t off[5];
+  layout(type, N, K, off);
+  const uint8_t* b = (const uint8_t*)buf;
+  const Mat m{{b + off[0], b + off[1], b + off[2], b + off[3]}, b + off[4], N, K / 256, N / 8};
+  const hipStream_t st = stream_of(s);
+  // three columns run as two launches (columns 0-1, then column 2), each with its own rows of y
+  auto run = [&](const int8_t* q, const float* d, float* yy, int nc) {
+    switch (type) {
+      case kQ4K: launch_nc<kQ4K>(m, q, d, yy, K, nc, st); break;
+      case kQ6K: launch_nc<kQ6K>(m, q, d, yy, K, nc, st); break;
+      case kIQ3S: launch_nc<kIQ3S>(m, q, d, yy, K, nc, st); break;
+      default: launch_nc<kIQ4XS>(m, q, d, yy, K, nc, st); break;
+    }
+  };
+  if (ncols == 3) {
+    run(xq, xd, y, 2);
+    run(xq + (size_t)2 * K, xd + (size_t)2 * (K / 32), y + (size_t)2 * N, 1);
+  } else {
+    run(xq, xd, y, ncols);
+  }
+  return check_launch("qgemv");
+}

@@ -136,3 +136,50 @@ def add_norm_rows(x, partial, recv, n, M, w, eps, h, xq, xd, xs, s=None):
 # ---------------------------------------------------------------- qmat.h
 def quantize_q8_1(x, xq, xd, K, ncols, s=None, xs=None):
     check(lib().q27h_quantize_q8_1(_ptr(x), _ptr(xq), _ptr(xd), K, ncols, _stream(s), _ptr(xs)))
+
+
+# Weight types of the decode GEMV: ggml type ids (src/gguf.h:12-14).
+Q4_K, Q6_K, IQ3_S, IQ4_XS = 12, 14, 21, 23
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, IQ3_S: 110, IQ4_XS: 136}
+
+
+class QMat:
+    """A quantized weight matrix on the GPU in the tile layout (src/qmat.h:19-29): `buf` is a torch uint8 device
+    tensor owning the repacked bytes."""
+
+    def __init__(self, type, N, K, buf):
+        self.type, self.N, self.K, self.buf = type, N, K, buf
+        self.nb, self.ntiles, self.bytes = K // 256, N // 8, buf.numel()
+
+
+def qmat_bytes(type, N, K):
+    return int(lib().q27h_qmat_bytes(type, N, K))
+
+
+def qmat_supported(type):
+    return type in BLOCK_BYTES
+
+
+def qmat_upload(raw, type, N, K, s=None):
+    """Repack N raw GGUF rows (a torch uint8 tensor on the device, [N][K/256] blocks) into a new QMat
+    (src/qmat.h:34, qmat_upload after its host-to-device copy)."""
+    import torch
+
+    nbytes = qmat_bytes(type, N, K)
+    if nbytes == 0:
+        check(lib().q27h_qmat_repack(type, N, K, None, None, _stream(s)))  # raises with the reason
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=raw.device)
+    check(lib().q27h_qmat_repack(type, N, K, _ptr(raw), _ptr(buf), _stream(s)))
+    return QMat(type, N, K, buf)
+
+
+def qmat_free(m):
+    m.buf = None
+
+
+def qgemv(m, xq, xd, y, ncols, s=None):
+    check(lib().q27h_qgemv(m.type, m.N, m.K, _ptr(m.buf), _ptr(xq), _ptr(xd), _ptr(y), ncols, _stream(s)))
+
+
+def qgemv_waves(N, K):
+    return int(lib().q27h_qgemv_waves(N, K))

@@ -87,3 +87,30 @@ def rope3_grid(text_before=3, nx=64, ny=64):
     for i in range(nx * ny):
         rows.append((p, p + i // nx, p + i % nx))
     return np.array(rows, np.int32).reshape(-1)
+
+
+# ---------------------------------------------------------------- decode GEMV weights (ggml type ids)
+Q4_K, Q6_K, IQ3_S, IQ4_XS = 12, 14, 21, 23
+QG_BLOCK = {Q4_K: 144, Q6_K: 210, IQ3_S: 110, IQ4_XS: 136}
+QG_D_OFFSETS = {Q4_K: (0, 2), Q6_K: (208,), IQ3_S: (0,), IQ4_XS: (0,)}
+QG_NAMES = {Q4_K: "q4_k", Q6_K: "q6_k", IQ3_S: "iq3_s", IQ4_XS: "iq4_xs"}
+# decode GEMV shapes of the model (N outputs x K inputs, tp = 1): wk/wv, ssm_out / wo, gate z, qkv, wq, ffn up/gate,
+# ffn down
+QG_SHAPES = [(1024, 5120), (5120, 6144), (6144, 5120), (10240, 5120), (12288, 5120), (17408, 5120), (5120, 17408)]
+
+
+def random_weights(r, type_, N, K, d_range=(-10, -4)):
+    """N rows of K/256 random blocks of a GEMV weight type, fp16 scale fields finite in 2^d_range."""
+    bb = QG_BLOCK[type_]
+    nblk = N * (K // 256)
+    t = r.integers(0, 256, nblk * bb, dtype=np.uint8).reshape(nblk, bb)
+    for off in QG_D_OFFSETS[type_]:
+        d = np.exp2(r.uniform(d_range[0], d_range[1], nblk)).astype(np.float16)
+        t[:, off:off + 2] = d.view(np.uint8).reshape(nblk, 2)
+    return t.reshape(-1)
+
+
+def q8_activations(oracle, r, ncols, K, std=1.0):
+    x = normal(r, ncols * K, std)
+    xq, xd, _ = oracle.quantize_q8_1(x, K, ncols)
+    return xq, xd

@@ -101,3 +101,21 @@ void step(float* x, const float* part, const float* w, float* h, int8_t* xq, flo
     r = subprocess.run(["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{inc}", "-I/opt/rocm/include",
                         str(src)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_qgemv_rejects_before_enqueue(q27):
+    L = q27.lib()
+    assert L.q27h_qgemv(8, 64, 256, FAKE, FAKE, FAKE, FAKE, 1, None) == -2  # Q8_0: not a GEMV type
+    assert "not supported" in L.q27h_last_error().decode()
+    assert L.q27h_qgemv(12, 60, 256, FAKE, FAKE, FAKE, FAKE, 1, None) == -1  # N % 8
+    assert L.q27h_qgemv(12, 64, 300, FAKE, FAKE, FAKE, FAKE, 1, None) == -1  # K % 256
+    assert L.q27h_qgemv(12, 64, 256, FAKE, FAKE, FAKE, FAKE, 5, None) == -1  # ncols
+    assert L.q27h_qgemv(12, 64, 256, FAKE + 16, FAKE, FAKE, FAKE, 1, None) == -4  # buf alignment
+    assert L.q27h_qmat_repack(14, 64, 256, FAKE, FAKE + 8, None) == -4
+    assert L.q27h_qmat_repack(21, 64, 250, FAKE, FAKE, None) == -1
+    # bytes: fields then scales, each 256-byte aligned (Q4_K 128 + 16 per chunk, 32 per (tile, block))
+    ntb = (64 // 8) * (512 // 256)
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert L.q27h_qmat_bytes(12, 64, 512) == al(ntb * 8 * 128) + al(ntb * 8 * 16) + al(ntb * 32)
+    assert L.q27h_qmat_bytes(23, 64, 512) == al(ntb * 8 * 128) + al(ntb * 8 * 8) + al(ntb * 16)
+    assert L.q27h_qmat_bytes(8, 64, 512) == 0

@@ -1,0 +1,114 @@
+"""GPU parity of the decode GEMV (q27h_qmat_repack + q27h_qgemv through the C ABI) against the CPU oracle:
+bit-exact y for every weight type, the model's shapes and 1..4 activation columns."""
+import sys
+
+import numpy as np
+import pytest
+
+import cfgdata as cd
+from conftest import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [cd.Q4_K, cd.Q6_K, cd.IQ4_XS, cd.IQ3_S]
+
+
+def say(msg):
+    print(f"[gpu-qgemv] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _run(q27, dev, type_, N, K, raw, xq, xd, ncols):
+    import torch
+
+    draw = torch.from_numpy(raw).to(dev)
+    m = q27.ops.qmat_upload(draw, type_, N, K)
+    y = torch.full((ncols * N,), float("nan"), device=dev)
+    q27.ops.qgemv(m, torch.from_numpy(xq).to(dev), torch.from_numpy(xd).to(dev), y, ncols)
+    torch.cuda.synchronize()
+    return y.cpu().numpy().reshape(ncols, N)
+
+
+@pytest.mark.parametrize("type_", TYPES)
+@pytest.mark.parametrize("shape", [(1024, 5120), (6144, 5120), (12288, 5120), (5120, 17408)])
+def test_qgemv_model_shapes(q27, oracle, dev, type_, shape):
+    N, K = shape
+    ncols = 4
+    say(f"qgemv type {type_} N={N} K={K} ncols={ncols}")
+    r = cd.rng(300 + type_ + N + K)
+    raw = cd.random_weights(r, type_, N, K)
+    xq, xd = cd.q8_activations(oracle, r, ncols, K)
+    got = _run(q27, dev, type_, N, K, raw, xq, xd, ncols)
+    want = oracle.qgemv(type_, raw, N, K, xq, xd, ncols)
+    assert_bits_equal(got, want, f"qgemv type {type_} {N}x{K}")
+
+
+@pytest.mark.parametrize("type_", TYPES)
+@pytest.mark.parametrize("ncols", [1, 2, 3])
+def test_qgemv_columns(q27, oracle, dev, type_, ncols):
+    N, K = 2048, 1536  # odd number of 8-block groups per row, W = 4
+    say(f"qgemv type {type_} ncols={ncols}")
+    r = cd.rng(400 + type_ + ncols)
+    raw = cd.random_weights(r, type_, N, K)
+    xq, xd = cd.q8_activations(oracle, r, ncols, K, std=3.0)
+    got = _run(q27, dev, type_, N, K, raw, xq, xd, ncols)
+    want = oracle.qgemv(type_, raw, N, K, xq, xd, ncols)
+    assert_bits_equal(got, want, f"qgemv type {type_} ncols {ncols}")
+
+
+def test_qgemv_small_and_edge_shapes(q27, oracle, dev):
+    """One tile, one block per row, and partial 8-block groups; zero activations and wide scale ranges."""
+    for type_ in TYPES:
+        for N, K in [(8, 256), (16, 768), (40, 2304)]:
+            say(f"qgemv edge type {type_} {N}x{K}")
+            r = cd.rng(500 + type_ + N)
+            raw = cd.random_weights(r, type_, N, K, d_range=(-24, 15))
+            xq, xd = cd.q8_activations(oracle, r, 2, K, std=50.0)
+            xq[: K // 2] = 0
+            got = _run(q27, dev, type_, N, K, raw, xq, xd, 2)
+            want = oracle.qgemv(type_, raw, N, K, xq, xd, 2)
+            assert_bits_equal(got, want, f"qgemv edge type {type_} {N}x{K}")
+
+
+def test_qgemv_errors(q27, dev):
+    import torch
+
+    from qwen27_engine_amd._lib import Q27Error
+
+    raw = torch.zeros(144 * 8, dtype=torch.uint8, device=dev)
+    with pytest.raises(Q27Error):
+        q27.ops.qmat_upload(raw, 8, 8, 256)  # Q8_0 is not a GEMV type
+    m = q27.ops.qmat_upload(raw, cd.Q4_K, 8, 256)
+    xq = torch.zeros(5 * 256, dtype=torch.int8, device=dev)
+    xd = torch.zeros(5 * 8, device=dev)
+    y = torch.zeros(5 * 8, device=dev)
+    with pytest.raises(Q27Error):
+        q27.ops.qgemv(m, xq, xd, y, 5)
+    assert q27.ops.qmat_bytes(cd.Q4_K, 12, 256) == 0  # N % 8
+
+
+def test_qgemv_replays_in_hip_graph(q27, oracle, dev):
+    import torch
+
+    say("qgemv graph replay")
+    type_, N, K, ncols = cd.IQ3_S, 1024, 5120, 4
+    r = cd.rng(600)
+    raw = cd.random_weights(r, type_, N, K)
+    xq, xd = cd.q8_activations(oracle, r, ncols, K)
+    m = q27.ops.qmat_upload(torch.from_numpy(raw).to(dev), type_, N, K)
+    dxq, dxd = torch.from_numpy(xq).to(dev), torch.from_numpy(xd).to(dev)
+    y = torch.zeros(ncols * N, device=dev)
+    want = oracle.qgemv(type_, raw, N, K, xq, xd, ncols).reshape(-1)
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        q27.ops.qgemv(m, dxq, dxd, y, ncols)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            q27.ops.qgemv(m, dxq, dxd, y, ncols)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_bits_equal(y.cpu().numpy(), want, "qgemv graph replay")
