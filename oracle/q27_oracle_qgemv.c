@@ -39,11 +39,12 @@ int q27o_qgemv_block_bytes(int type) {
   }
 }
 
-/* Waves per 8-row tile: a function of the shape only, so results do not depend on the device. */
+/* Waves per 8-row tile: a function of the shape only (ceil(K / 2048), at most 4), so results do not depend on the
+ * device. */
 int q27o_qgemv_waves(int N, int K) {
-  (void)K;
-  const int ntiles = N / 8;
-  return ntiles >= 1536 ? 1 : ntiles >= 768 ? 2 : 4;
+  (void)N;
+  const int nb = K / 256;
+  return nb >= 32 ? 4 : (nb + 7) / 8 < 1 ? 1 : (nb + 7) / 8;
 }
 
 static float h2f(const uint8_t* p) { return q27o_h2f((uint16_t)(p[0] | (p[1] << 8))); }

@@ -5,8 +5,7 @@
 // by row inside the tile; the super-block scales go to an array ordered by (tile, block), then row. The repack only
 // moves bytes, so every weight decodes to the value it has in the GGUF block.
 //
-// Kernel (gfx950): a 256-thread workgroup = 4 waves. W waves (1, 2 or 4, a function of the shape only) share one
-// tile; lane l = 8 lb + s of wave w takes sub-block s of the blocks b = 8 w + lb, + 8 W, ... and keeps the 8 rows x
+// Kernel (gfx950): one workgroup of W waves per tile (W = 1..4, a function of K only); lane l = 8 lb + s of wave w takes sub-block s of the blocks b = 8 w + lb, + 8 W, ... and keeps the 8 rows x
 // ncols partial sums in registers, so one load of its 32 activations per column serves 8 rows. Integer dot products
 // per sub-block use v_dot4_i32_i8 (exact); the float contribution of each sub-block is the reference's expression of
 // that type (src/qgemv.cu:369-560). The 64 lane sums are added as an xor butterfly in which each exchange level sends
@@ -49,17 +48,32 @@ struct Mat {
   int N, nb, ntiles;
 };
 
+// Where the bytes of a chunk's field go. Fields of up to 16 bytes per chunk are stored chunk after chunk (chunk
+// index (tile * nb + b) * 8 + s), so the 32 chunks of 4 consecutive blocks are contiguous. Wider fields are cut in
+// 16-byte pieces and, per tile, per group of 4 blocks, piece i of the group's 32 chunks lies together: one 16-byte
+// load per lane of a half-wave (4 blocks x 8 sub-blocks) then reads 512 contiguous bytes. A tile's block count is
+// padded to a multiple of 4 for these fields.
+__host__ __device__ __forceinline__ size_t field_off(int wf, size_t tile, int nb, int b, int s) {
+  if (wf <= 16) return ((tile * nb + b) * 8 + s) * wf;
+  const size_t g = tile * ((nb + 3) / 4) + b / 4;
+  return (g * (wf / 16) * 32 + (b % 4) * 8 + s) * 16;  // + piece i at i * 512
+}
+__host__ __device__ constexpr size_t field_bytes(int wf, size_t ntiles, int nb) {
+  return wf <= 16 ? ntiles * nb * 8 * wf : ntiles * ((nb + 3) / 4) * 32 * wf;
+}
+
 // Field offsets inside the QMat buffer: the fields in order, then the scales, each 256-byte aligned.
 size_t layout(int type, int N, int K, size_t off[5]) {
   const Fmt F = fmt_of(type);
-  const size_t ntb = (size_t)(N / 8) * (K / 256);
+  const size_t ntiles = N / 8;
+  const int nb = K / 256;
   size_t o = 0;
   for (int i = 0; i < 4; i++) {
     off[i] = o;
-    if (i < F.nf) o += align256(ntb * 8 * F.w[i]);
+    if (i < F.nf) o += align256(field_bytes(F.w[i], ntiles, nb));
   }
   off[4] = o;
-  return o + align256(ntb * F.dw);
+  return o + align256(ntiles * nb * F.dw);
 }
 
 // ---------------------------------------------------------------- repack (one thread per chunk)
@@ -74,9 +88,8 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restri
   const size_t tb = chunk >> 3;
   const int b = (int)(tb % nb);
   const size_t tile = tb / nb;
-  uint8_t* o0 = f0 + chunk * F.w[0];
-  uint8_t* o1 = f1 + chunk * F.w[1];
-  uint8_t* o2 = F.nf > 2 ? f2 + chunk * F.w[2] : nullptr;
+  // the chunk's records (8 rows each), then scattered to the field layout
+  uint8_t o0[F.w[0]], o1[F.w[1]], o2[F.w[2] ? F.w[2] : 1];
   uint32_t nib = 0;
   for (int r = 0; r < 8; r++) {
     const uint8_t* src = raw + ((tile * 8 + r) * nb + b) * F.bb;
@@ -140,20 +153,38 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restri
       }
     }
   }
-  if constexpr (TYPE == kIQ3S) *(uint32_t*)(f3 + chunk * 4) = nib;
+  auto put = [&](uint8_t* f, int wf, const uint8_t* rec) {
+    uint8_t* dst = f + field_off(wf, tile, nb, b, s);
+    for (int k = 0; k < wf; k++) dst[(wf <= 16 ? 0 : (k / 16) * 512) + (wf <= 16 ? k : k % 16)] = rec[k];
+  };
+  put(f0, F.w[0], o0);
+  put(f1, F.w[1], o1);
+  if constexpr (F.nf > 2) put(f2, F.w[2], o2);
+  if constexpr (TYPE == kIQ3S) *(uint32_t*)(f3 + field_off(4, tile, nb, b, s)) = nib;
 }
 
 // ---------------------------------------------------------------- decode of one chunk
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+// Exact integer product of operands within 24 bits whose product fits 32 bits (v_mul_i32_i24, full rate; a plain
+// 32-bit multiply is a quarter-rate instruction). Every product below satisfies both bounds: |sum of a sub-block| <
+// 2^19 and |scale| < 2^7.
+__device__ __forceinline__ int mul24(int a, int b) { return ((a << 8) >> 8) * ((b << 8) >> 8); }
 __device__ __forceinline__ float half_lo(uint32_t w) { return h2f_bits((uint16_t)(w & 0xFFFF)); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f_bits((uint16_t)(w >> 16)); }
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#ifndef Q27H_QG_NT
+#define Q27H_QG_NT 1
+#endif
 template <int N>
 __device__ __forceinline__ void ld16(uint32_t* w, const uint8_t* p) {  // N x 16 bytes, streaming (read once)
 #pragma unroll
   for (int i = 0; i < N; i++) {
+#if Q27H_QG_NT
     const u32x4 v = __builtin_nontemporal_load((const u32x4*)p + i);
+#else
+    const u32x4 v = ((const u32x4*)p)[i];
+#endif
     w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
   }
 }
@@ -181,28 +212,35 @@ struct Chunk {
   uint32_t w[nw];
 };
 
+// N 16-byte pieces of a field wider than 16 bytes (pieces 512 bytes apart, see field_off)
+template <int N>
+__device__ __forceinline__ void ldp(uint32_t* w, const uint8_t* p) {
+#pragma unroll
+  for (int i = 0; i < N; i++) ld16<1>(w + 4 * i, p + 512 * i);
+}
+
 template <int TYPE>
-__device__ __forceinline__ void load_chunk(Chunk<TYPE>& c, const Mat& m, size_t tb, int s) {
-  const size_t ch = tb * 8 + s;
+__device__ __forceinline__ void load_chunk(Chunk<TYPE>& c, const Mat& m, size_t tile, int b, int s) {
+  const size_t tb = tile * m.nb + b;
   if constexpr (TYPE == kQ4K) {
-    ld16<8>(c.w, m.f[0] + ch * 128);
-    ld16<1>(c.w + 32, m.f[1] + ch * 16);
+    ldp<8>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
+    ld16<1>(c.w + 32, m.f[1] + field_off(16, tile, m.nb, b, s));
     ld16<2>(c.w + 36, m.d + tb * 32);
   } else if constexpr (TYPE == kQ6K) {
-    ld16<8>(c.w, m.f[0] + ch * 128);
-    ld16<4>(c.w + 32, m.f[1] + ch * 64);
-    ld16<1>(c.w + 48, m.f[2] + ch * 16);
+    ldp<8>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
+    ldp<4>(c.w + 32, m.f[1] + field_off(64, tile, m.nb, b, s));
+    ld16<1>(c.w + 48, m.f[2] + field_off(16, tile, m.nb, b, s));
     ld16<1>(c.w + 52, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ3S) {
-    ld16<4>(c.w, m.f[0] + ch * 64);
-    ld16<2>(c.w + 16, m.f[1] + ch * 32);
-    const u32x2 h = __builtin_nontemporal_load((const u32x2*)(m.f[2] + ch * 8));
+    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ldp<2>(c.w + 16, m.f[1] + field_off(32, tile, m.nb, b, s));
+    const u32x2 h = *(const u32x2*)(m.f[2] + field_off(8, tile, m.nb, b, s));
     c.w[24] = h.x; c.w[25] = h.y;
-    c.w[26] = __builtin_nontemporal_load((const uint32_t*)(m.f[3] + ch * 4));
+    c.w[26] = *(const uint32_t*)(m.f[3] + field_off(4, tile, m.nb, b, s));
     ld16<1>(c.w + 27, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ4XS) {
-    ld16<8>(c.w, m.f[0] + ch * 128);
-    const u32x2 l = __builtin_nontemporal_load((const u32x2*)(m.f[1] + ch * 8));
+    ldp<8>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
+    const u32x2 l = *(const u32x2*)(m.f[1] + field_off(8, tile, m.nb, b, s));
     c.w[32] = l.x; c.w[33] = l.y;
     ld16<1>(c.w + 34, m.d + tb * 16);
   }
@@ -239,7 +277,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const float d = half_lo(w[36 + r]), dmin = half_hi(w[36 + r]);
 #pragma unroll
       for (int c = 0; c < NC; c++)
-        acc[r * NC + c] += d * (dy[c] * (float)(sumi[c] * sc)) - dmin * (dy[c] * (float)(s8[c] * mn));
+        acc[r * NC + c] += d * (dy[c] * (float)mul24(sumi[c], sc)) - dmin * (dy[c] * (float)mul24(s8[c], mn));
     }
   } else if constexpr (TYPE == kQ6K) {
     int s8a[NC], s8b[NC];  // activation sums of the two 16-weight halves (the -32 offset of the quants)
@@ -276,7 +314,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const float d = (r & 1) ? half_hi(w[52 + r / 2]) : half_lo(w[52 + r / 2]);
 #pragma unroll
       for (int c = 0; c < NC; c++) {
-        const int si = (sa[c] - 32 * s8a[c]) * sc0 + (sb[c] - 32 * s8b[c]) * sc1;
+        const int si = mul24(sa[c] - 32 * s8a[c], sc0) + mul24(sb[c] - 32 * s8b[c], sc1);
         acc[r * NC + c] += d * (dy[c] * (float)si);
       }
     }
@@ -298,7 +336,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const int mul = 1 + 2 * (int)((w[26] >> (4 * r)) & 0xF);
       const float d = (r & 1) ? half_hi(w[27 + r / 2]) : half_lo(w[27 + r / 2]);
 #pragma unroll
-      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)(sumi[c] * mul);
+      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)mul24(sumi[c], mul);
     }
   } else if constexpr (TYPE == kIQ4XS) {
 #pragma unroll
@@ -316,7 +354,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const int ls = (int)(int8_t)((w[32 + r / 4] >> (8 * (r & 3))) & 0xFF);
       const float d = (r & 1) ? half_hi(w[34 + r / 2]) : half_lo(w[34 + r / 2]);
 #pragma unroll
-      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)(sumi[c] * ls);
+      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)mul24(sumi[c], ls);
     }
   }
 }
@@ -327,29 +365,30 @@ __device__ __forceinline__ float xchg(float v) {
   if constexpr (O == 32) return lane_xor32(v);
   else return lane_xor<O>(v);
 }
-// One butterfly level: lanes with bit O set keep the upper half of the live values, the others the lower half;
-// each adds the partner's copy of the same values.
-template <int O, int V>
-__device__ __forceinline__ void reduce_level(float (&a)[V], int& cur, int lane) {
-  if (cur > 1) {
-    const int h = cur / 2;
-    const bool up = (lane & O) != 0;
+// One butterfly level over the first CUR live values: lanes with bit O set keep the upper half, the others the lower
+// half; each adds the partner's copy of the same values. The two candidates are chosen with bit masks (v_bfi), so no
+// value is ever selected by a per-lane index (which the compiler would lower to a compare chain over all values).
+template <int O, int CUR, int V>
+__device__ __forceinline__ void reduce_level(float (&a)[V], int lane) {
+  if constexpr (CUR > 1) {
+    constexpr int h = CUR / 2;
+    const int up = (lane & O) ? -1 : 0;
 #pragma unroll
-    for (int i = 0; i < V / 2; i++) {
-      if (i < h) {
-        const float send = up ? a[i] : a[i + h];
-        const float keep = up ? a[i + h] : a[i];
-        a[i] = keep + xchg<O>(send);
-      }
+    for (int i = 0; i < h; i++) {
+      const int lo = __builtin_bit_cast(int, a[i]), hi = __builtin_bit_cast(int, a[i + h]);
+      const float send = __builtin_bit_cast(float, (lo & up) | (hi & ~up));
+      const float keep = __builtin_bit_cast(float, (hi & up) | (lo & ~up));
+      a[i] = keep + xchg<O>(send);
     }
-    cur = h;
   } else {
     a[0] += xchg<O>(a[0]);
   }
 }
-
-constexpr int waves_per_tile(int N) {
-  return N / 8 >= 1536 ? 1 : N / 8 >= 768 ? 2 : 4;
+// Waves per tile: enough for every lane to take at most one block of each tile for K <= 8192, at most 4 (the
+// workgroup is these W waves). A function of K only; part of the summation order.
+constexpr int waves_per_tile(int K) {
+  const int nb = K / 256;
+  return nb >= 32 ? 4 : (nb + 7) / 8 < 1 ? 1 : (nb + 7) / 8;
 }
 
 template <int TYPE, int NC>
@@ -358,7 +397,7 @@ __global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restr
   __shared__ uint32_t lut[TYPE == kIQ3S ? 512 : 1];
   __shared__ float part[4][8 * NC];
   if constexpr (TYPE == kIQ3S) {
-    for (int i = threadIdx.x; i < 512; i += 256) lut[i] = kIQ3SGrid[i];
+    for (int i = threadIdx.x; i < 512; i += blockDim.x) lut[i] = kIQ3SGrid[i];
   }
   uint32_t kv[4] = {0, 0, 0, 0};
   if constexpr (TYPE == kIQ4XS) {
@@ -369,8 +408,8 @@ __global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restr
   }
   if constexpr (TYPE == kIQ3S) __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int tile = blockIdx.x * (4 / W) + wave / W;
-  const int wv = wave % W;
+  const int tile = blockIdx.x;
+  const int wv = wave;
   const int lb = lane >> 3, s = lane & 7;
   const bool live = tile < m.ntiles;  // uniform per wave
   float acc[8 * NC];
@@ -379,7 +418,7 @@ __global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restr
   if (live) {
     for (int b = 8 * wv + lb; b < m.nb; b += 8 * W) {
       Chunk<TYPE> ch;
-      load_chunk<TYPE>(ch, m, (size_t)tile * m.nb + b, s);
+      load_chunk<TYPE>(ch, m, (size_t)tile, b, s);
       int u[NC][8];
       float dy[NC];
 #pragma unroll
@@ -395,13 +434,14 @@ __global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restr
   }
   // 64-lane butterfly; afterwards lane l holds value index l >> (6 - log2(8 NC)) (copies in the lower lane bits)
   constexpr int V = 8 * NC;
-  int cur = V;
-  reduce_level<32>(acc, cur, lane);
-  reduce_level<16>(acc, cur, lane);
-  reduce_level<8>(acc, cur, lane);
-  reduce_level<4>(acc, cur, lane);
-  reduce_level<2>(acc, cur, lane);
-  reduce_level<1>(acc, cur, lane);
+  constexpr int c1 = V, c2 = c1 > 1 ? c1 / 2 : 1, c3 = c2 > 1 ? c2 / 2 : 1, c4 = c3 > 1 ? c3 / 2 : 1,
+                c5 = c4 > 1 ? c4 / 2 : 1, c6 = c5 > 1 ? c5 / 2 : 1;
+  reduce_level<32, c1>(acc, lane);
+  reduce_level<16, c2>(acc, lane);
+  reduce_level<8, c3>(acc, lane);
+  reduce_level<4, c4>(acc, lane);
+  reduce_level<2, c5>(acc, lane);
+  reduce_level<1, c6>(acc, lane);
   constexpr int shift = V == 8 ? 3 : V == 16 ? 2 : V == 32 ? 1 : 0;  // NC = 3 (V = 24) is handled on the host
   const int idx = lane >> shift;
   const bool writer = (lane & ((1 << shift) - 1)) == 0;
@@ -425,9 +465,9 @@ int check_type(int type) {
 
 template <int TYPE, int NC>
 void launch_gemv(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, hipStream_t s) {
-  const int W = waves_per_tile(m.N);
-  const int grid = (m.ntiles * W + 3) / 4;
-  hipLaunchKernelGGL((qgemv_kernel<TYPE, NC>), dim3(grid), dim3(256), 0, s, m, xq, xd, y, K, W);
+  const int W = waves_per_tile(K);
+  const int grid = m.ntiles;
+  hipLaunchKernelGGL((qgemv_kernel<TYPE, NC>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
 }
 
 template <int TYPE>
@@ -449,8 +489,8 @@ extern "C" size_t q27h_qmat_bytes(int type, int N, int K) {
 }
 
 extern "C" int q27h_qgemv_waves(int N, int K) {
-  (void)K;
-  return waves_per_tile(N);
+  (void)N;
+  return waves_per_tile(K);
 }
 
 extern "C" int q27h_qmat_repack(int type, int N, int K, const void* raw, void* buf, q27h_stream_t s) {

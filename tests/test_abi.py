@@ -113,9 +113,11 @@ def test_qgemv_rejects_before_enqueue(q27):
     assert L.q27h_qgemv(12, 64, 256, FAKE + 16, FAKE, FAKE, FAKE, 1, None) == -4  # buf alignment
     assert L.q27h_qmat_repack(14, 64, 256, FAKE, FAKE + 8, None) == -4
     assert L.q27h_qmat_repack(21, 64, 250, FAKE, FAKE, None) == -1
-    # bytes: fields then scales, each 256-byte aligned (Q4_K 128 + 16 per chunk, 32 per (tile, block))
+    # bytes: fields then scales, each 256-byte aligned (Q4_K 128 + 16 per chunk, 32 per (tile, block)); ntb at K = 512
     ntb = (64 // 8) * (512 // 256)
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert L.q27h_qmat_bytes(12, 64, 512) == al(ntb * 8 * 128) + al(ntb * 8 * 16) + al(ntb * 32)
-    assert L.q27h_qmat_bytes(23, 64, 512) == al(ntb * 8 * 128) + al(ntb * 8 * 8) + al(ntb * 16)
+    assert L.q27h_qmat_bytes(12, 64, 1024) == al(2 * ntb * 8 * 128) + al(2 * ntb * 8 * 16) + al(2 * ntb * 32)
+    assert L.q27h_qmat_bytes(23, 64, 1024) == al(2 * ntb * 8 * 128) + al(2 * ntb * 8 * 8) + al(2 * ntb * 16)
+    # fields wider than 16 bytes per chunk pad a tile's blocks to a multiple of 4 (K = 512: 2 blocks -> 4)
+    assert L.q27h_qmat_bytes(12, 64, 512) == al(2 * ntb * 8 * 128) + al(ntb * 8 * 16) + al(ntb * 32)
     assert L.q27h_qmat_bytes(8, 64, 512) == 0

@@ -46,7 +46,7 @@ def test_qgemv_model_shapes(q27, oracle, dev, type_, shape):
 @pytest.mark.parametrize("type_", TYPES)
 @pytest.mark.parametrize("ncols", [1, 2, 3])
 def test_qgemv_columns(q27, oracle, dev, type_, ncols):
-    N, K = 2048, 1536  # odd number of 8-block groups per row, W = 4
+    N, K = 2048, 1536  # 6 blocks per row: one wave, slots 6 and 7 idle
     say(f"qgemv type {type_} ncols={ncols}")
     r = cd.rng(400 + type_ + ncols)
     raw = cd.random_weights(r, type_, N, K)
