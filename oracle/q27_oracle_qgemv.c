@@ -43,8 +43,8 @@ int q27o_qgemv_block_bytes(int type) {
  * device. */
 int q27o_qgemv_waves(int N, int K) {
   (void)N;
-  const int nb = K / 256;
-  return nb >= 32 ? 4 : (nb + 7) / 8 < 1 ? 1 : (nb + 7) / 8;
+  const int w = (K / 256 + 7) / 8;
+  return w < 1 ? 1 : w > 4 ? 4 : w;
 }
 
 static float h2f(const uint8_t* p) { return q27o_h2f((uint16_t)(p[0] | (p[1] << 8))); }

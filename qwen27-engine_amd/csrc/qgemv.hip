@@ -189,13 +189,6 @@ __device__ __forceinline__ void ld16(uint32_t* w, const uint8_t* p) {  // N x 16
   }
 }
 
-// Bytes of g negated where the matching bit of the 4-bit mask is set (g's bytes are magnitudes 1..127, so
-// two's complement per byte, (b ^ 0xFF) + 1, never carries into the next byte).
-__device__ __forceinline__ int signed_bytes(uint32_t g, uint32_t nib4) {
-  const uint32_t ones = ((nib4 & 1u) | ((nib4 & 2u) << 7) | ((nib4 & 4u) << 14) | ((nib4 & 8u) << 21));
-  return (int)((g ^ (ones * 0xFFu)) + ones);
-}
-
 // IQ4_XS levels of 4 nibbles (one per byte, values 0..15) via two byte permutes of the 16-entry table.
 __device__ __forceinline__ int iq4_levels(uint32_t nib, const uint32_t (&t)[4]) {
   const uint32_t sel = nib & 0x07070707u;
@@ -319,19 +312,28 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       }
     }
   } else if constexpr (TYPE == kIQ3S) {
+    // lut[0..511] = the codebook, lut[512..1023] = per sign byte the byte masks (0x00 / 0xFF) of its two nibbles
+    const uint2* smask = (const uint2*)(lut + 512);
 #pragma unroll
     for (int r = 0; r < 8; r++) {
       const uint32_t qh = (w[24 + r / 4] >> (8 * (r & 3))) & 0xFF;
       const uint32_t sg = w[16 + r];
+      // all 12 table reads of the row first, then the arithmetic: one LDS wait per row instead of one per lookup
+      uint32_t g[8];
+      uint2 mm[4];
+#pragma unroll
+      for (int k = 0; k < 8; k++) g[k] = lut[((w[2 * r + k / 4] >> (8 * (k & 3))) & 0xFF) | ((qh << (8 - k)) & 0x100)];
+#pragma unroll
+      for (int p = 0; p < 4; p++) mm[p] = smask[(sg >> (8 * p)) & 0xFF];
       int sumi[NC];
 #pragma unroll
       for (int c = 0; c < NC; c++) sumi[c] = 0;
 #pragma unroll
       for (int k = 0; k < 8; k++) {
-        const uint32_t idx = ((w[2 * r + k / 4] >> (8 * (k & 3))) & 0xFF) | ((qh << (8 - k)) & 0x100);
-        const int g = signed_bytes(lut[idx], (sg >> (4 * k)) & 0xF);
+        const uint32_t m = (k & 1) ? mm[k / 2].y : mm[k / 2].x;
+        const int gs = (int)((g[k] ^ m) + (m & 0x01010101u));  // negated bytes: (b ^ 0xFF) + 1, no carry (b >= 1)
 #pragma unroll
-        for (int c = 0; c < NC; c++) sumi[c] = dot4(g, u[c][k], sumi[c]);
+        for (int c = 0; c < NC; c++) sumi[c] = dot4(gs, u[c][k], sumi[c]);
       }
       const int mul = 1 + 2 * (int)((w[26] >> (4 * r)) & 0xF);
       const float d = (r & 1) ? half_hi(w[27 + r / 2]) : half_lo(w[27 + r / 2]);
@@ -384,20 +386,30 @@ __device__ __forceinline__ void reduce_level(float (&a)[V], int lane) {
     a[0] += xchg<O>(a[0]);
   }
 }
-// Waves per tile: enough for every lane to take at most one block of each tile for K <= 8192, at most 4 (the
+// Waves per tile: enough for every lane to take at most one block of each tile (ceil(K / 2048)), at most 4 (the
 // workgroup is these W waves). A function of K only; part of the summation order.
+constexpr int kMaxW = 4;
 constexpr int waves_per_tile(int K) {
-  const int nb = K / 256;
-  return nb >= 32 ? 4 : (nb + 7) / 8 < 1 ? 1 : (nb + 7) / 8;
+  const int w = (K / 256 + 7) / 8;
+  return w < 1 ? 1 : w > kMaxW ? kMaxW : w;
 }
 
 template <int TYPE, int NC>
-__global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+__global__ void __launch_bounds__(64 * kMaxW) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                     float* __restrict__ y, int K, int W) {
-  __shared__ uint32_t lut[TYPE == kIQ3S ? 512 : 1];
-  __shared__ float part[4][8 * NC];
+  __shared__ uint32_t lut[TYPE == kIQ3S ? 1024 : 1];
+  __shared__ float part[kMaxW][8 * NC];
   if constexpr (TYPE == kIQ3S) {
     for (int i = threadIdx.x; i < 512; i += blockDim.x) lut[i] = kIQ3SGrid[i];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {  // sign byte -> byte masks of its low and high nibble
+      uint32_t m0 = 0, m1 = 0;
+      for (int j = 0; j < 4; j++) {
+        m0 |= ((i >> j) & 1) ? 0xFFu << (8 * j) : 0u;
+        m1 |= ((i >> (4 + j)) & 1) ? 0xFFu << (8 * j) : 0u;
+      }
+      lut[512 + 2 * i] = m0;
+      lut[513 + 2 * i] = m1;
+    }
   }
   uint32_t kv[4] = {0, 0, 0, 0};
   if constexpr (TYPE == kIQ4XS) {

@@ -59,7 +59,7 @@ def test_qgemv_columns(q27, oracle, dev, type_, ncols):
 def test_qgemv_small_and_edge_shapes(q27, oracle, dev):
     """One tile, one block per row, and partial 8-block groups; zero activations and wide scale ranges."""
     for type_ in TYPES:
-        for N, K in [(8, 256), (16, 768), (40, 2304)]:
+        for N, K in [(8, 256), (16, 768), (40, 2304), (16, 40960)]:
             say(f"qgemv edge type {type_} {N}x{K}")
             r = cd.rng(500 + type_ + N)
             raw = cd.random_weights(r, type_, N, K, d_range=(-24, 15))
