@@ -418,6 +418,49 @@ def bench_multimodal(q27, torch, M=4099):
     return res
 
 
+GEMV_TYPES = {"iq3_s": (21, 110, (0,)), "q4_k": (12, 144, (0, 2)), "q6_k": (14, 210, (208,)), "iq4_xs": (23, 136, (0,))}
+# decode GEMV shapes of the model (N outputs x K inputs, tp = 1): wk / wv, ssm_out / wo, gate z, qkv, wq,
+# ffn up / gate, ffn down (src/model.cu:715-796)
+GEMV_SHAPES = [(1024, 5120), (5120, 6144), (6144, 5120), (10240, 5120), (12288, 5120), (17408, 5120), (5120, 17408)]
+
+
+def bench_gemv(q27, torch):
+    """Decode GEMV (the consumer of the q8_1 activations, src/qgemv.cu): per weight type and model shape, us per
+    launch and GB/s of (matrix bytes + activations + y) with T = 4 and T = 1 activation columns. Enough distinct
+    matrices are cycled that no launch finds its weights in the 256 MB MALL (as in a decode step, which streams
+    all 64 layers' weights)."""
+    import math
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    out = {}
+    for name, (tid, bb, doffs) in GEMV_TYPES.items():
+        res = {}
+        for N, K in (GEMV_SHAPES if name == "iq3_s" else [(17408, 5120), (5120, 17408)]):
+            nbytes = q27.ops.qmat_bytes(tid, N, K)
+            cnt = max(3, math.ceil(600e6 / nbytes))
+            raw = torch.randint(0, 256, (N * (K // 256), bb), dtype=torch.uint8, device=dev, generator=g)
+            for off in doffs:
+                d = torch.exp2(torch.rand(raw.shape[0], device=dev, generator=g) * 6 - 10).to(torch.float16)
+                raw[:, off:off + 2] = d.view(torch.uint8).view(-1, 2)
+            mats = [q27.ops.qmat_upload(raw.reshape(-1), tid, N, K) for _ in range(cnt)]
+            del raw
+            for nc in (4, 1):
+                xq = torch.randint(-127, 128, (nc * K,), dtype=torch.int8, device=dev, generator=g)
+                xd = torch.rand(nc * K // 32, device=dev, generator=g) * 0.01
+                y = torch.empty(nc * N, device=dev)
+                us = time_back_to_back(torch, lambda i: q27.ops.qgemv(mats[i % cnt], xq, xd, y, nc), 3 * cnt)
+                b = nbytes + nc * K * (1 + 4 / 32) + nc * N * 4
+                res[f"{N}x{K}_T{nc}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                                         "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 3), "matrix_MB": round(nbytes / 1e6, 2)}
+                log(f"  gemv {name:6s} {N:6d}x{K:<6d} T={nc} {us:7.2f} us {b / us / 1e3:7.1f} GB/s")
+            del mats
+            torch.cuda.empty_cache()
+        out[name] = res
+    return out
+
+
 def bench_cfg1(q27, torch):
     """RMSNorm -> q8_1 of one 5120 row (0.1% outliers x50) on the CPU oracle and on the GPU, with the
     bit-exact comparison of xq / xd / xs."""
@@ -610,6 +653,8 @@ def main():
     torch.cuda.empty_cache()
     multimodal = bench_multimodal(q27, torch)
     torch.cuda.empty_cache()
+    gemv = bench_gemv(q27, torch)
+    torch.cuda.empty_cache()
 
     if args.calib_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -650,6 +695,7 @@ def main():
         "cfg1_rmsnorm_q8_row": cfg1,
         "gathers_cfg4": gathers,
         "multimodal_cfg5": multimodal,
+        "decode_gemv": gemv,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

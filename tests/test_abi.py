@@ -96,6 +96,12 @@ void step(float* x, const float* part, const float* w, float* h, int8_t* xq, flo
   q27::gdn_flip_plane(plane, s);
   (void)q27::kv_cache_bytes(4, 180224, true);
 }
+void decode_gemv(const void* raw, const int8_t* xq, const float* xd, float* y, hipStream_t s) {
+  q27::QMat m = q27::qmat_upload_raw(q27::GType::IQ3_S, 17408, 5120, raw, s);  // src/qmat.h:34 (device half)
+  q27::qgemv(m, xq, xd, y, 4, s);                                                // src/qmat.h:44-46
+  q27::qmat_free(m);
+  (void)q27::qmat_supported(q27::GType::Q4_K);
+}
 ''')
     inc = os.path.join(ROOT, "include")
     r = subprocess.run(["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{inc}", "-I/opt/rocm/include",
