@@ -428,20 +428,37 @@ __global__ void __launch_bounds__(64 * kMaxW) qgemv_kernel(Mat m, const int8_t* 
 #pragma unroll
   for (int i = 0; i < 8 * NC; i++) acc[i] = 0.0f;
   if (live) {
-    for (int b = 8 * wv + lb; b < m.nb; b += 8 * W) {
-      Chunk<TYPE> ch;
-      load_chunk<TYPE>(ch, m, (size_t)tile, b, s);
-      int u[NC][8];
-      float dy[NC];
+    // Blocks b, b + step, ... of this lane, software-pipelined: the next chunk is requested right after the current
+    // block's activations (so waiting for those does not wait for the prefetch; loads return in order) and before
+    // the current chunk is decoded. Past the last block the prefetch re-reads the current block (a cache hit), so
+    // every load is unconditional.
+    const int step = 8 * W;
+    int b = 8 * wv + lb;
+    Chunk<TYPE> ca, cb;
+    int u[NC][8];
+    float dy[NC];
+    auto load_x = [&](int bb) {
 #pragma unroll
       for (int c = 0; c < NC; c++) {
-        const int4* xp = (const int4*)(xq + (size_t)c * K + (size_t)b * 256 + s * 32);
+        const int4* xp = (const int4*)(xq + (size_t)c * K + (size_t)bb * 256 + s * 32);
         const int4 a0 = xp[0], a1 = xp[1];
         u[c][0] = a0.x; u[c][1] = a0.y; u[c][2] = a0.z; u[c][3] = a0.w;
         u[c][4] = a1.x; u[c][5] = a1.y; u[c][6] = a1.z; u[c][7] = a1.w;
-        dy[c] = xd[(size_t)c * (K / 32) + b * 8 + s];
+        dy[c] = xd[(size_t)c * (K / 32) + bb * 8 + s];
       }
-      dot_chunk<TYPE, NC>(ch, u, dy, lut, kv, acc);
+    };
+    if (b < m.nb) load_chunk<TYPE>(ca, m, (size_t)tile, b, s);
+    while (b < m.nb) {
+      load_x(b);
+      const int b1 = b + step;
+      load_chunk<TYPE>(cb, m, (size_t)tile, b1 < m.nb ? b1 : b, s);
+      dot_chunk<TYPE, NC>(ca, u, dy, lut, kv, acc);
+      if (b1 >= m.nb) break;
+      load_x(b1);
+      const int b2 = b1 + step;
+      load_chunk<TYPE>(ca, m, (size_t)tile, b2 < m.nb ? b2 : b1, s);
+      dot_chunk<TYPE, NC>(cb, u, dy, lut, kv, acc);
+      b = b2;
     }
   }
   // 64-lane butterfly; afterwards lane l holds value index l >> (6 - log2(8 NC)) (copies in the lower lane bits)
