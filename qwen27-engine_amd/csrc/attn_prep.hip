@@ -24,14 +24,15 @@ struct RopeFreqs {
 };
 
 
-// One wave per (token, group of HPW heads): HPW = 4 for batches (the 28 heads of a token are 7 waves, wave w taking
-// heads w, w + 7, w + 14, w + 21, so the 4 K heads with their q8/f16 cache work are spread over 4 waves instead of
-// making one wave the straggler), HPW = 1 for a few tokens, where the shorter chain per wave matters more than loads
-// in flight. The 32 rotary angles of the token are evaluated
+// One wave per (token, group of HPW heads): HPW = 2 for batches (the 28 heads of a token are 14 waves, wave w taking
+// heads w and w + 14, so the 4 K heads with their q8/f16 cache work are spread over 4 waves instead of making one
+// wave the straggler; measured 26.5 us against 28.9 us with 4 heads per wave at 2048 tokens), HPW = 1 for a few
+// tokens, where the shorter chain per wave matters more than loads in flight. The 32 rotary angles of the token are
+// evaluated
 // once per wave (lane j < 32 takes pair j) and handed to the lanes that need them with ds_bpermute; the head
 // vectors of the whole group are loaded before any arithmetic.
 #ifndef Q27H_ATTN_HPW
-#define Q27H_ATTN_HPW 4
+#define Q27H_ATTN_HPW 2
 #endif
 
 template <int HPW>

@@ -92,6 +92,11 @@ __device__ __forceinline__ void decode4<kQ80>(const uint8_t* __restrict__ b, int
   for (int j = 0; j < 4; j++) y[j] = (float)(int8_t)b[2 + r + j] * d;
 }
 
+#ifndef Q27H_NT_ROWS
+#define Q27H_NT_ROWS 0
+#endif
+constexpr bool kRowsNT = Q27H_NT_ROWS;
+
 template <int F>
 __global__ void __launch_bounds__(256) get_rows_kernel(const uint8_t* __restrict__ table, int64_t row_bytes,
                                                        const int* __restrict__ ids, float* __restrict__ y, int n,
@@ -125,7 +130,7 @@ __global__ void __launch_bounds__(256) get_rows_kernel(const uint8_t* __restrict
   for (int o = 4 * t; o < nv; o += 1024) {
     float v[4];
     decode4<F>((const uint8_t*)stage + (o / BV) * BB, o % BV, v);
-    *(float4*)(out + o) = make_float4(v[0], v[1], v[2], v[3]);
+    st4<kRowsNT>(out + o, v[0], v[1], v[2], v[3]);
   }
 }
 
