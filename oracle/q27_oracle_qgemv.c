@@ -11,10 +11,12 @@
  *   - the 64 lane sums of a wave are added as an xor butterfly (lane xor 32, 16, 8, 4, 2, 1);
  *   - the wave sums are added in wave order: ((P0 + P1) + P2) + P3.
  * The GPU kernel (qwen27-engine_amd/csrc/qgemv.hip) adds the same operands in the same order.
- * Block formats: ggml block_q4_K / block_q6_K / block_iq4_xs / block_iq3_s (ggml-common.h), the dequantization
- * order of src/requant.cpp:68-114 (Q6_K, Q4_K) and ggml's dequantize_row_iq4_xs / dequantize_row_iq3_s.
- * Parity: pinned by tests/test_oracle_qgemv.py (float64 dequantize-and-dot bound, one-hot integer cases, the
- * summation order replayed in numpy). */
+ * Block formats: ggml block_q2_K / q4_K / q6_K / iq2_xxs / iq2_xs / iq2_s / iq3_xxs / iq3_s / iq4_xs / iq1_m
+ * (ggml-common.h), the dequantization order of src/requant.cpp:68-114 (Q6_K, Q4_K) and ggml's dequantize_row_*; the
+ * integer scale rules of the IQ2 / IQ3_XXS types, including their truncating divisions, are the reference's
+ * (src/qgemv.cu:395-420, 492-545).
+ * Parity: pinned by tests/test_oracle_qgemv.py (exact-integer cases against numpy dequantizers, a float64
+ * dequantize-and-dot bound, the waves rule shared with the library). */
 #include <stdint.h>
 #include <string.h>
 
@@ -26,8 +28,38 @@ static const uint32_t kIQ3SGrid[512] = {
 static const int8_t kIQ4NL[16] = {
 #include "../qwen27-engine_amd/csrc/iq4nl_values.inc"
 };
+static const uint64_t kIQ2XXSGrid[256] = {
+#include "../qwen27-engine_amd/csrc/iq2xxs_grid.inc"
+};
+static const uint64_t kIQ2XSGrid[512] = {
+#include "../qwen27-engine_amd/csrc/iq2xs_grid.inc"
+};
+static const uint64_t kIQ2SGrid[1024] = {
+#include "../qwen27-engine_amd/csrc/iq2s_grid.inc"
+};
+static const uint32_t kIQ3XXSGrid[256] = {
+#include "../qwen27-engine_amd/csrc/iq3xxs_grid.inc"
+};
+static const uint32_t kIQ1SGrid[2048] = {
+#include "../qwen27-engine_amd/csrc/iq1s_grid.inc"
+};
 
-enum { T_Q4_K = 12, T_Q6_K = 14, T_IQ3_S = 21, T_IQ4_XS = 23 };
+enum {
+  T_Q2_K = 10, T_Q4_K = 12, T_Q6_K = 14, T_IQ2_XXS = 16, T_IQ2_XS = 17, T_IQ3_XXS = 18, T_IQ3_S = 21, T_IQ2_S = 22,
+  T_IQ4_XS = 23, T_IQ1_M = 29
+};
+
+/* 7 sign bits plus the parity bit that makes the count of negative signs even (ggml ksigns_iq2xs) */
+static int ksigns(int v7) { return v7 | ((__builtin_popcount(v7) & 1) << 7); }
+/* sum over the 8 magnitudes of a 64-bit grid entry (one byte each) times the signed activations */
+static int dot8(uint64_t g, int signs, const int8_t* u) {
+  int s = 0;
+  for (int j = 0; j < 8; j++) {
+    const int mag = (int)((g >> (8 * j)) & 0xFF);
+    s += ((signs >> j) & 1 ? -mag : mag) * u[j];
+  }
+  return s;
+}
 
 int q27o_qgemv_block_bytes(int type) {
   switch (type) {
@@ -35,6 +67,12 @@ int q27o_qgemv_block_bytes(int type) {
     case T_Q6_K: return 210;
     case T_IQ3_S: return 110;
     case T_IQ4_XS: return 136;
+    case T_Q2_K: return 84;
+    case T_IQ2_XXS: return 66;
+    case T_IQ2_XS: return 74;
+    case T_IQ3_XXS: return 98;
+    case T_IQ2_S: return 82;
+    case T_IQ1_M: return 56;
     default: return 0;
   }
 }
@@ -119,6 +157,98 @@ static float chunk_t(int type, const uint8_t* blk, int s, const int8_t* u, float
       }
     }
     return (d * dy) * (float)(sumi * mul);
+  }
+  if (type == T_Q2_K) {
+    /* scales[16], qs[64], d, dmin; sub s = 4 n + j: weights 128 n + 32 j + l = (qs[32 n + l] >> 2 j) & 3, the two
+     * 16-weight halves with scale byte scales[8 n + 2 j + h] (low nibble scale, high nibble min) */
+    const int n = s / 4, j = s % 4;
+    const float d = h2f(blk + 80), dmin = h2f(blk + 82);
+    const uint8_t g0 = blk[8 * n + 2 * j], g1 = blk[8 * n + 2 * j + 1];
+    int sa = 0, sb = 0, s8a = 0, s8b = 0;
+    for (int l = 0; l < 32; l++) {
+      const int q = (blk[16 + 32 * n + l] >> (2 * j)) & 3;
+      if (l < 16) { sa += q * u[l]; s8a += u[l]; }
+      else { sb += q * u[l]; s8b += u[l]; }
+    }
+    const int sd = sa * (g0 & 0xF) + sb * (g1 & 0xF);
+    const int smn = s8a * (g0 >> 4) + s8b * (g1 >> 4);
+    return d * (dy * (float)sd) - dmin * (dy * (float)smn);
+  }
+  if (type == T_IQ2_XXS) {
+    /* d, then per sub-block 4 grid index bytes and a word of 4 x 7 sign bits + a 4-bit scale (top bits) */
+    const float d = h2f(blk);
+    const uint8_t* q = blk + 2 + 8 * s;
+    const uint32_t aux = (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) | ((uint32_t)q[7] << 24);
+    int sumi = 0;
+    for (int p = 0; p < 4; p++) sumi += dot8(kIQ2XXSGrid[q[p]], ksigns((aux >> (7 * p)) & 0x7F), u + 8 * p);
+    const int ls = (int)((aux >> 27) | 1);
+    return (d * dy) * (float)(sumi * ls / 8);
+  }
+  if (type == T_IQ2_XS || type == T_IQ2_S) {
+    const float d = h2f(blk);
+    int s0 = 0, s1 = 0, lsb;
+    for (int p = 0; p < 4; p++) {
+      int gi, sb;
+      if (type == T_IQ2_XS) {  /* d, qs[32] (u16: 9-bit grid index, 7 sign bits), scales[8] */
+        const int q16 = blk[2 + 8 * s + 2 * p] | (blk[3 + 8 * s + 2 * p] << 8);
+        gi = q16 & 0x1FF;
+        sb = ksigns(q16 >> 9);
+      } else {  /* d, qs[32], signs[32], qh[8], scales[8]: 10-bit index = qs | 2 bits of qh */
+        gi = blk[2 + 4 * s + p] | ((blk[66 + s] << (8 - 2 * p)) & 0x300);
+        sb = blk[34 + 4 * s + p];
+      }
+      const int v = dot8(type == T_IQ2_XS ? kIQ2XSGrid[gi] : kIQ2SGrid[gi], sb, u + 8 * p);
+      if (p < 2) s0 += v;
+      else s1 += v;
+    }
+    lsb = blk[(type == T_IQ2_XS ? 66 : 74) + s];
+    const int si = (s0 * (lsb & 0xF) + s1 * (lsb >> 4) + (s0 + s1) / 2) / 4;
+    return (d * dy) * (float)si;
+  }
+  if (type == T_IQ3_XXS) {
+    /* d, qs[64] (grid indices, 8 per sub-block), then per sub-block a word of 4 x 7 sign bits + 4-bit scale */
+    const float d = h2f(blk);
+    const uint8_t* qs = blk + 2 + 8 * s;
+    const uint8_t* a = blk + 66 + 4 * s;
+    const uint32_t aux = (uint32_t)a[0] | ((uint32_t)a[1] << 8) | ((uint32_t)a[2] << 16) | ((uint32_t)a[3] << 24);
+    int sumi = 0;
+    for (int p = 0; p < 4; p++) {
+      const int sb = ksigns((aux >> (7 * p)) & 0x7F);
+      const uint64_t g = (uint64_t)kIQ3XXSGrid[qs[2 * p]] | ((uint64_t)kIQ3XXSGrid[qs[2 * p + 1]] << 32);
+      sumi += dot8(g, sb, u + 8 * p);
+    }
+    const int ls = (int)(aux >> 28);
+    const int si = (ls * sumi + sumi / 2) / 2;
+    return (d * dy) * (float)si;
+  }
+  if (type == T_IQ1_M) {
+    /* qs[32], qh[16], scales[8] (4 x u16; the fp16 super-block scale is their four top nibbles). Grid entries hold
+     * 8 nibbles g (value + 1); each group of 8 weights adds delta * (sum of its activations) with delta = -7/8 or
+     * -9/8 by bit 3 of the group's qh nibble. */
+    uint16_t s16[4];
+    for (int k = 0; k < 4; k++) s16[k] = (uint16_t)(blk[48 + 2 * k] | (blk[49 + 2 * k] << 8));
+    const uint16_t dh = (uint16_t)((s16[0] >> 12) | ((s16[1] >> 8) & 0x00F0) | ((s16[2] >> 4) & 0x0F00) | (s16[3] & 0xF000));
+    const float dw = q27o_h2f(dh);
+    const int qh16 = blk[32 + 2 * s] | (blk[33 + 2 * s] << 8);
+    const int sc6 = (s16[s / 2] >> (6 * (s % 2))) & 63;
+    int si[2] = {0, 0};
+    float sf[2] = {0.0f, 0.0f};
+    for (int p = 0; p < 4; p++) {
+      const int qhl = (qh16 >> (4 * p)) & 0xF;
+      const uint32_t grid = kIQ1SGrid[blk[4 * s + p] | ((qhl & 7) << 8)];
+      int sy = 0, dotp = 0;
+      for (int jj = 0; jj < 8; jj++) {
+        /* nibble order of the GPU grid: bytes of (grid & 0x0F0F0F0F) are weights 0..3, of (grid >> 4) weights 4..7 */
+        const int g = jj < 4 ? (int)((grid >> (8 * jj)) & 0xF) : (int)((grid >> (8 * (jj - 4) + 4)) & 0xF);
+        dotp += g * u[8 * p + jj];
+        sy += u[8 * p + jj];
+      }
+      const float delta = -1.0f + 0.125f - (float)(qhl & 0x08) * (2.0f * 0.125f / 8.0f);
+      si[p / 2] += dotp;
+      sf[p / 2] += delta * (float)sy;
+    }
+    const int sc0 = 2 * (sc6 & 7) + 1, sc1 = 2 * ((sc6 >> 3) & 7) + 1;
+    return (dw * dy) * ((((float)si[0] + sf[0]) * (float)sc0) + (((float)si[1] + sf[1]) * (float)sc1));
   }
   return 0.0f;
 }

@@ -90,10 +90,23 @@ def rope3_grid(text_before=3, nx=64, ny=64):
 
 
 # ---------------------------------------------------------------- decode GEMV weights (ggml type ids)
-Q4_K, Q6_K, IQ3_S, IQ4_XS = 12, 14, 21, 23
-QG_BLOCK = {Q4_K: 144, Q6_K: 210, IQ3_S: 110, IQ4_XS: 136}
-QG_D_OFFSETS = {Q4_K: (0, 2), Q6_K: (208,), IQ3_S: (0,), IQ4_XS: (0,)}
-QG_NAMES = {Q4_K: "q4_k", Q6_K: "q6_k", IQ3_S: "iq3_s", IQ4_XS: "iq4_xs"}
+Q2_K, Q4_K, Q6_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ1_M = 10, 12, 14, 16, 17, 18, 21, 22, 23, 29
+QG_TYPES = [Q2_K, Q4_K, Q6_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ1_M]
+QG_BLOCK = {Q2_K: 84, Q4_K: 144, Q6_K: 210, IQ2_XXS: 66, IQ2_XS: 74, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ4_XS: 136,
+            IQ1_M: 56}
+# fp16 scale fields inside a block (IQ1_M has none: its scale is the four top nibbles of the scales words)
+QG_D_OFFSETS = {Q2_K: (80, 82), Q4_K: (0, 2), Q6_K: (208,), IQ2_XXS: (0,), IQ2_XS: (0,), IQ3_XXS: (0,), IQ3_S: (0,),
+                IQ2_S: (0,), IQ4_XS: (0,), IQ1_M: ()}
+QG_NAMES = {Q2_K: "q2_k", Q4_K: "q4_k", Q6_K: "q6_k", IQ2_XXS: "iq2_xxs", IQ2_XS: "iq2_xs", IQ3_XXS: "iq3_xxs",
+            IQ3_S: "iq3_s", IQ2_S: "iq2_s", IQ4_XS: "iq4_xs", IQ1_M: "iq1_m"}
+
+
+def set_iq1m_scale(blocks, h16):
+    """Write fp16 bit patterns h16 [nblk] as the IQ1_M super-block scale: nibble k of h16 is the top nibble of the
+    scales word k (bytes 48 + 2 k, 49 + 2 k)."""
+    for k in range(4):
+        nib = ((h16.astype(np.uint32) >> (4 * k)) & 0xF).astype(np.uint8)
+        blocks[:, 49 + 2 * k] = (blocks[:, 49 + 2 * k] & 0x0F) | (nib << 4)
 # decode GEMV shapes of the model (N outputs x K inputs, tp = 1): wk/wv, ssm_out / wo, gate z, qkv, wq, ffn up/gate,
 # ffn down
 QG_SHAPES = [(1024, 5120), (5120, 6144), (6144, 5120), (10240, 5120), (12288, 5120), (17408, 5120), (5120, 17408)]
@@ -107,6 +120,8 @@ def random_weights(r, type_, N, K, d_range=(-10, -4)):
     for off in QG_D_OFFSETS[type_]:
         d = np.exp2(r.uniform(d_range[0], d_range[1], nblk)).astype(np.float16)
         t[:, off:off + 2] = d.view(np.uint8).reshape(nblk, 2)
+    if type_ == IQ1_M:
+        set_iq1m_scale(t, np.exp2(r.uniform(d_range[0], d_range[1], nblk)).astype(np.float16).view(np.uint16))
     return t.reshape(-1)
 
 
