@@ -418,7 +418,9 @@ def bench_multimodal(q27, torch, M=4099):
     return res
 
 
-GEMV_TYPES = {"iq3_s": (21, 110, (0,)), "q4_k": (12, 144, (0, 2)), "q6_k": (14, 210, (208,)), "iq4_xs": (23, 136, (0,))}
+GEMV_TYPES = {"iq3_s": (21, 110, (0,)), "q4_k": (12, 144, (0, 2)), "q6_k": (14, 210, (208,)), "iq4_xs": (23, 136, (0,)),
+              "q2_k": (10, 84, (80, 82)), "iq2_xxs": (16, 66, (0,)), "iq2_xs": (17, 74, (0,)), "iq3_xxs": (18, 98, (0,)),
+              "iq2_s": (22, 82, (0,)), "iq1_m": (29, 56, ())}
 # decode GEMV shapes of the model (N outputs x K inputs, tp = 1): wk / wv, ssm_out / wo, gate z, qkv, wq,
 # ffn up / gate, ffn down (src/model.cu:715-796)
 GEMV_SHAPES = [(1024, 5120), (5120, 6144), (6144, 5120), (10240, 5120), (12288, 5120), (17408, 5120), (5120, 17408)]
@@ -444,6 +446,9 @@ def bench_gemv(q27, torch):
             for off in doffs:
                 d = torch.exp2(torch.rand(raw.shape[0], device=dev, generator=g) * 6 - 10).to(torch.float16)
                 raw[:, off:off + 2] = d.view(torch.uint8).view(-1, 2)
+            if name == "iq1_m":  # the fp16 scale is the four top nibbles of the scales words: keep it finite
+                raw[:, 49:56:2] &= 0x0F
+                raw[:, 55] |= 0x20
             mats = [q27.ops.qmat_upload(raw.reshape(-1), tid, N, K) for _ in range(cnt)]
             del raw
             for nc in (4, 1):

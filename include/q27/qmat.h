@@ -2,7 +2,8 @@
 // the quantized weight matrix QMat, its upload / free, the decode GEMV qgemv and the q8_1 activation quantizer,
 // forwarding to include/q27h.h. Bad shapes and unsupported types throw std::runtime_error, as the reference does.
 //
-// Weight types of qgemv here: Q4_K, Q6_K, IQ3_S, IQ4_XS (q27h_qmat_bytes returns 0 for the others). The prefill
+// Weight types of qgemv: the ten of the reference (Q2_K, Q4_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_XS,
+// IQ1_M; q27h_qmat_bytes returns 0 for the others). The prefill
 // GEMM (qgemm) and qmat_upload_shard (the two-GPU split) of the reference are not part of this library.
 // GType / GTensor come from the engine's own gguf.h when it is on the include path; otherwise this header declares
 // the ggml type ids it needs and only the raw-rows upload is available.

@@ -134,7 +134,8 @@ int q27h_get_rows_q8_0(const uint8_t* table, int64_t row_bytes, const int* ids, 
                        const float* img);
 
 /* ---------------------------------------------------------------- decode GEMV over quantized weights
- * Weight types are ggml type ids (src/gguf.h:12-14): 12 Q4_K, 14 Q6_K, 21 IQ3_S, 23 IQ4_XS. A matrix of N rows
+ * Weight types are the ggml type ids of the reference's GEMV (src/gguf.h:12-14, src/qgemv.cu:63-71): 10 Q2_K, 12 Q4_K,
+ * 14 Q6_K, 16 IQ2_XXS, 17 IQ2_XS, 18 IQ3_XXS, 21 IQ3_S, 22 IQ2_S, 23 IQ4_XS, 29 IQ1_M. A matrix of N rows
  * (outputs, N % 8 == 0) and K columns (K % 256 == 0) lives in one caller-owned device buffer in the tile layout
  * of the reference's QMat (src/qmat.h:1-8).
  * q27h_qmat_bytes (src/qmat.h:31): bytes of that buffer (0 for an unsupported type or shape). */

@@ -1,5 +1,6 @@
 // Decode GEMV over quantized weights (the consumer of the q8_1 activations): y[c][n] = sum_k W[n][k] x[c][k] for
-// 1..4 activation columns, W in GGUF block types Q4_K, Q6_K, IQ3_S and IQ4_XS repacked into the tile layout of the
+// 1..4 activation columns, W in the ten GGUF block types of the reference (Q2_K, Q4_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S,
+// IQ3_XXS, IQ3_S, IQ4_XS, IQ1_M) repacked into the tile layout of the
 // reference's QMat (src/qmat.h:1-8): 8 rows per tile; chunk = (tile, 256-weight block b, 32-weight sub-block s),
 // chunk index (tile * nb + b) * 8 + s; every field of the block struct goes to its own array ordered by chunk, then
 // by row inside the tile; the super-block scales go to an array ordered by (tile, block), then row. The repack only
@@ -17,10 +18,26 @@
 namespace q27h {
 namespace {
 
-constexpr int kQ4K = 12, kQ6K = 14, kIQ3S = 21, kIQ4XS = 23;
+constexpr int kQ2K = 10, kQ4K = 12, kQ6K = 14, kIQ2XXS = 16, kIQ2XS = 17, kIQ3XXS = 18, kIQ3S = 21, kIQ2S = 22,
+              kIQ4XS = 23, kIQ1M = 29;
 
 __device__ const uint32_t kIQ3SGrid[512] = {
 #include "iq3s_grid.inc"
+};
+__device__ const uint32_t kIQ3XXSGrid[256] = {
+#include "iq3xxs_grid.inc"
+};
+__device__ const uint64_t kIQ2XXSGrid[256] = {
+#include "iq2xxs_grid.inc"
+};
+__device__ const uint64_t kIQ2XSGrid[512] = {
+#include "iq2xs_grid.inc"
+};
+__device__ const uint64_t kIQ2SGrid[1024] = {
+#include "iq2s_grid.inc"
+};
+__device__ const uint32_t kIQ1SGrid[2048] = {
+#include "iq1s_grid.inc"
 };
 __device__ const int8_t kIQ4NL[16] = {
 #include "iq4nl_values.inc"
@@ -34,11 +51,17 @@ struct Fmt {
   int bb;
 };
 __host__ __device__ constexpr Fmt fmt_of(int type) {
-  return type == kQ4K    ? Fmt{2, {128, 16, 0, 0}, 32, 144}
-         : type == kQ6K  ? Fmt{3, {128, 64, 16, 0}, 16, 210}
-         : type == kIQ3S ? Fmt{4, {64, 32, 8, 4}, 16, 110}
-         : type == kIQ4XS ? Fmt{2, {128, 8, 0, 0}, 16, 136}
-                          : Fmt{0, {0, 0, 0, 0}, 0, 0};
+  return type == kQ2K      ? Fmt{2, {64, 16, 0, 0}, 32, 84}
+         : type == kQ4K    ? Fmt{2, {128, 16, 0, 0}, 32, 144}
+         : type == kQ6K    ? Fmt{3, {128, 64, 16, 0}, 16, 210}
+         : type == kIQ2XXS ? Fmt{1, {64, 0, 0, 0}, 16, 66}
+         : type == kIQ2XS  ? Fmt{2, {64, 8, 0, 0}, 16, 74}
+         : type == kIQ3XXS ? Fmt{2, {64, 32, 0, 0}, 16, 98}
+         : type == kIQ3S   ? Fmt{4, {64, 32, 8, 4}, 16, 110}
+         : type == kIQ2S   ? Fmt{4, {32, 32, 8, 8}, 16, 82}
+         : type == kIQ4XS  ? Fmt{2, {128, 8, 0, 0}, 16, 136}
+         : type == kIQ1M   ? Fmt{3, {32, 16, 8, 0}, 16, 56}
+                           : Fmt{0, {0, 0, 0, 0}, 0, 0};
 }
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -89,7 +112,7 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restri
   const int b = (int)(tb % nb);
   const size_t tile = tb / nb;
   // the chunk's records (8 rows each), then scattered to the field layout
-  uint8_t o0[F.w[0]], o1[F.w[1]], o2[F.w[2] ? F.w[2] : 1];
+  uint8_t o0[F.w[0]], o1[F.w[1] ? F.w[1] : 1], o2[F.w[2] ? F.w[2] : 1], o3[F.w[3] ? F.w[3] : 1];
   uint32_t nib = 0;
   for (int r = 0; r < 8; r++) {
     const uint8_t* src = raw + ((tile * 8 + r) * nb + b) * F.bb;
@@ -151,6 +174,62 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restri
         od[2 * r] = src[0];
         od[2 * r + 1] = src[1];
       }
+    } else if constexpr (TYPE == kQ2K) {  // scales[16], qs[64], d, dmin
+      // sub-block s = 4 n + j: weights 128 n + 32 j + l = (qs[32 n + l] >> 2 j) & 3. Word h (weights 16 h ..):
+      // byte k holds weights 16 h + k + 4 i at bits 2 i.
+      const int n = s / 4, j = s % 4;
+      const uint8_t* qs = src + 16 + 32 * n;
+      for (int h = 0; h < 2; h++)
+        for (int k = 0; k < 4; k++) {
+          uint8_t v = 0;
+          for (int i = 0; i < 4; i++) v |= (uint8_t)(((qs[16 * h + k + 4 * i] >> (2 * j)) & 3) << (2 * i));
+          o0[8 * r + 4 * h + k] = v;
+        }
+      o1[2 * r] = src[8 * n + 2 * j];
+      o1[2 * r + 1] = src[8 * n + 2 * j + 1];
+      if (s == 0)
+        for (int k = 0; k < 4; k++) od[4 * r + k] = src[80 + k];
+    } else if constexpr (TYPE == kIQ2XXS) {  // d, per sub-block 4 grid indices + a sign / scale word
+      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
+      if (s == 0) {
+        od[2 * r] = src[0];
+        od[2 * r + 1] = src[1];
+      }
+    } else if constexpr (TYPE == kIQ2XS) {  // d, qs[32] (u16 index + signs), scales[8]
+      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
+      o1[r] = src[66 + s];
+      if (s == 0) {
+        od[2 * r] = src[0];
+        od[2 * r + 1] = src[1];
+      }
+    } else if constexpr (TYPE == kIQ3XXS) {  // d, qs[64], scales_and_signs[32]
+      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
+      for (int k = 0; k < 4; k++) o1[4 * r + k] = src[66 + 4 * s + k];
+      if (s == 0) {
+        od[2 * r] = src[0];
+        od[2 * r + 1] = src[1];
+      }
+    } else if constexpr (TYPE == kIQ2S) {  // d, qs[32], signs[32], qh[8], scales[8]
+      for (int k = 0; k < 4; k++) o0[4 * r + k] = src[2 + 4 * s + k];
+      for (int k = 0; k < 4; k++) o1[4 * r + k] = src[34 + 4 * s + k];
+      o2[r] = src[66 + s];
+      o3[r] = src[74 + s];
+      if (s == 0) {
+        od[2 * r] = src[0];
+        od[2 * r + 1] = src[1];
+      }
+    } else if constexpr (TYPE == kIQ1M) {  // qs[32], qh[16], scales[8] (4 x u16, fp16 scale in the top nibbles)
+      for (int k = 0; k < 4; k++) o0[4 * r + k] = src[4 * s + k];
+      o1[2 * r] = src[32 + 2 * s];
+      o1[2 * r + 1] = src[33 + 2 * s];
+      uint16_t s16[4];
+      for (int k = 0; k < 4; k++) s16[k] = (uint16_t)(src[48 + 2 * k] | (src[49 + 2 * k] << 8));
+      o2[r] = (uint8_t)((s16[s / 2] >> (6 * (s % 2))) & 63);
+      if (s == 0) {
+        const uint16_t dh = (uint16_t)((s16[0] >> 12) | ((s16[1] >> 8) & 0x00F0) | ((s16[2] >> 4) & 0x0F00) | (s16[3] & 0xF000));
+        od[2 * r] = (uint8_t)(dh & 0xFF);
+        od[2 * r + 1] = (uint8_t)(dh >> 8);
+      }
     }
   }
   auto put = [&](uint8_t* f, int wf, const uint8_t* rec) {
@@ -158,9 +237,10 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restri
     for (int k = 0; k < wf; k++) dst[(wf <= 16 ? 0 : (k / 16) * 512) + (wf <= 16 ? k : k % 16)] = rec[k];
   };
   put(f0, F.w[0], o0);
-  put(f1, F.w[1], o1);
+  if constexpr (F.nf > 1) put(f1, F.w[1], o1);
   if constexpr (F.nf > 2) put(f2, F.w[2], o2);
   if constexpr (TYPE == kIQ3S) *(uint32_t*)(f3 + field_off(4, tile, nb, b, s)) = nib;
+  else if constexpr (F.nf > 3) put(f3, F.w[3], o3);
 }
 
 // ---------------------------------------------------------------- decode of one chunk
@@ -197,6 +277,16 @@ __device__ __forceinline__ int iq4_levels(uint32_t nib, const uint32_t (&t)[4]) 
   const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
   return (int)((hi & m) | (lo & ~m));
 }
+
+// Tables of a type in LDS: `grid` words of codebook, then `masks` entries of two words (the 0x00 / 0xFF byte masks
+// of the low and high nibble of a sign byte; 128 entries = ksigns of 7 bits, 256 = the byte itself).
+template <int TYPE>
+struct LutInfo {
+  static constexpr int grid = TYPE == kIQ3S ? 512 : TYPE == kIQ2XXS ? 512 : TYPE == kIQ2XS ? 1024 : TYPE == kIQ2S ? 2048
+                              : TYPE == kIQ3XXS ? 256 : TYPE == kIQ1M ? 2048 : 0;
+  static constexpr int masks = TYPE == kIQ3S || TYPE == kIQ2S ? 256 : TYPE == kIQ2XXS || TYPE == kIQ2XS || TYPE == kIQ3XXS ? 128 : 0;
+  static constexpr int words = grid + 2 * masks;
+};
 
 template <int TYPE>
 struct Chunk {
@@ -236,6 +326,36 @@ __device__ __forceinline__ void load_chunk(Chunk<TYPE>& c, const Mat& m, size_t 
     const u32x2 l = *(const u32x2*)(m.f[1] + field_off(8, tile, m.nb, b, s));
     c.w[32] = l.x; c.w[33] = l.y;
     ld16<1>(c.w + 34, m.d + tb * 16);
+  } else if constexpr (TYPE == kQ2K) {
+    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ld16<1>(c.w + 16, m.f[1] + field_off(16, tile, m.nb, b, s));
+    ld16<2>(c.w + 20, m.d + tb * 32);
+  } else if constexpr (TYPE == kIQ2XXS) {
+    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ld16<1>(c.w + 16, m.d + tb * 16);
+  } else if constexpr (TYPE == kIQ2XS) {
+    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    const u32x2 l = *(const u32x2*)(m.f[1] + field_off(8, tile, m.nb, b, s));
+    c.w[16] = l.x; c.w[17] = l.y;
+    ld16<1>(c.w + 18, m.d + tb * 16);
+  } else if constexpr (TYPE == kIQ3XXS) {
+    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ldp<2>(c.w + 16, m.f[1] + field_off(32, tile, m.nb, b, s));
+    ld16<1>(c.w + 24, m.d + tb * 16);
+  } else if constexpr (TYPE == kIQ2S) {
+    ldp<2>(c.w, m.f[0] + field_off(32, tile, m.nb, b, s));
+    ldp<2>(c.w + 8, m.f[1] + field_off(32, tile, m.nb, b, s));
+    const u32x2 h = *(const u32x2*)(m.f[2] + field_off(8, tile, m.nb, b, s));
+    c.w[16] = h.x; c.w[17] = h.y;
+    const u32x2 l = *(const u32x2*)(m.f[3] + field_off(8, tile, m.nb, b, s));
+    c.w[18] = l.x; c.w[19] = l.y;
+    ld16<1>(c.w + 20, m.d + tb * 16);
+  } else if constexpr (TYPE == kIQ1M) {
+    ldp<2>(c.w, m.f[0] + field_off(32, tile, m.nb, b, s));
+    ld16<1>(c.w + 8, m.f[1] + field_off(16, tile, m.nb, b, s));
+    const u32x2 l = *(const u32x2*)(m.f[2] + field_off(8, tile, m.nb, b, s));
+    c.w[12] = l.x; c.w[13] = l.y;
+    ld16<1>(c.w + 14, m.d + tb * 16);
   }
 }
 
@@ -313,7 +433,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
     }
   } else if constexpr (TYPE == kIQ3S) {
     // lut[0..511] = the codebook, lut[512..1023] = per sign byte the byte masks (0x00 / 0xFF) of its two nibbles
-    const uint2* smask = (const uint2*)(lut + 512);
+    const uint2* smask = (const uint2*)(lut + LutInfo<TYPE>::grid);
 #pragma unroll
     for (int r = 0; r < 8; r++) {
       const uint32_t qh = (w[24 + r / 4] >> (8 * (r & 3))) & 0xFF;
@@ -358,6 +478,162 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
 #pragma unroll
       for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)mul24(sumi[c], ls);
     }
+  } else if constexpr (TYPE == kQ2K) {
+    int s8a[NC], s8b[NC];  // activation sums of the two 16-weight halves (the min terms multiply them)
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      int ta = 0, tb = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        ta = dot4(u[c][k], 0x01010101, ta);
+        tb = dot4(u[c][k + 4], 0x01010101, tb);
+      }
+      s8a[c] = ta;
+      s8b[c] = tb;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      int sa[NC], sb[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) sa[c] = sb[c] = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int va = (int)((w[2 * r] >> (2 * i)) & 0x03030303u), vb = (int)((w[2 * r + 1] >> (2 * i)) & 0x03030303u);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          sa[c] = dot4(va, u[c][i], sa[c]);
+          sb[c] = dot4(vb, u[c][4 + i], sb[c]);
+        }
+      }
+      const uint32_t g = w[16 + r / 2] >> (16 * (r & 1));
+      const int g0 = (int)(g & 0xFF), g1 = (int)((g >> 8) & 0xFF);
+      const float d = half_lo(w[20 + r]), dmin = half_hi(w[20 + r]);
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const int sd = mul24(sa[c], g0 & 0xF) + mul24(sb[c], g1 & 0xF);
+        const int smn = mul24(s8a[c], g0 >> 4) + mul24(s8b[c], g1 >> 4);
+        acc[r * NC + c] += d * (dy[c] * (float)sd) - dmin * (dy[c] * (float)smn);
+      }
+    }
+  } else if constexpr (TYPE == kIQ2XXS || TYPE == kIQ2XS || TYPE == kIQ2S) {
+    // 64-bit codebook entries (8 magnitudes) in lut, then the byte masks of each sign byte (ksigns of 7 bits for
+    // IQ2_XXS / IQ2_XS, the stored byte for IQ2_S)
+    const uint2* grid = (const uint2*)lut;
+    const uint2* smask = (const uint2*)(lut + LutInfo<TYPE>::grid);
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      uint2 e[4], mm[4];
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        if constexpr (TYPE == kIQ2XXS) {
+          e[p] = grid[(w[2 * r] >> (8 * p)) & 0xFF];
+          mm[p] = smask[(w[2 * r + 1] >> (7 * p)) & 0x7F];
+        } else if constexpr (TYPE == kIQ2XS) {
+          const uint32_t q16 = (w[2 * r + p / 2] >> (16 * (p & 1))) & 0xFFFF;
+          e[p] = grid[q16 & 0x1FF];
+          mm[p] = smask[q16 >> 9];
+        } else {
+          const uint32_t qh = (w[16 + r / 4] >> (8 * (r & 3))) & 0xFF;
+          e[p] = grid[((w[r] >> (8 * p)) & 0xFF) | ((qh << (8 - 2 * p)) & 0x300)];
+          mm[p] = smask[(w[8 + r] >> (8 * p)) & 0xFF];
+        }
+      }
+      int s0[NC], s1[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) s0[c] = s1[c] = 0;
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int gx = (int)((e[p].x ^ mm[p].x) + (mm[p].x & 0x01010101u));
+        const int gy = (int)((e[p].y ^ mm[p].y) + (mm[p].y & 0x01010101u));
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          if (p < 2 || TYPE == kIQ2XXS) s0[c] = dot4(gy, u[c][2 * p + 1], dot4(gx, u[c][2 * p], s0[c]));
+          else s1[c] = dot4(gy, u[c][2 * p + 1], dot4(gx, u[c][2 * p], s1[c]));
+        }
+      }
+      if constexpr (TYPE == kIQ2XXS) {
+        const int ls = (int)((w[2 * r + 1] >> 27) | 1);
+        const float d = (r & 1) ? half_hi(w[16 + r / 2]) : half_lo(w[16 + r / 2]);
+#pragma unroll
+        for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)(mul24(s0[c], ls) / 8);
+      } else {
+        const uint32_t lsb = TYPE == kIQ2XS ? (w[16 + r / 4] >> (8 * (r & 3))) & 0xFF : (w[18 + r / 4] >> (8 * (r & 3))) & 0xFF;
+        const int ls0 = (int)(lsb & 0xF), ls1 = (int)(lsb >> 4);
+        constexpr int DW = TYPE == kIQ2XS ? 18 : 20;
+        const float d = (r & 1) ? half_hi(w[DW + r / 2]) : half_lo(w[DW + r / 2]);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          const int si = (mul24(s0[c], ls0) + mul24(s1[c], ls1) + (s0[c] + s1[c]) / 2) / 4;
+          acc[r * NC + c] += (d * dy[c]) * (float)si;
+        }
+      }
+    }
+  } else if constexpr (TYPE == kIQ3XXS) {
+    const uint2* smask = (const uint2*)(lut + LutInfo<TYPE>::grid);
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const uint32_t aux = w[16 + r];
+      uint32_t g[8];
+      uint2 mm[4];
+#pragma unroll
+      for (int k = 0; k < 8; k++) g[k] = lut[(w[2 * r + k / 4] >> (8 * (k & 3))) & 0xFF];
+#pragma unroll
+      for (int p = 0; p < 4; p++) mm[p] = smask[(aux >> (7 * p)) & 0x7F];
+      int sumi[NC];
+#pragma unroll
+      for (int c = 0; c < NC; c++) sumi[c] = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const uint32_t m = (k & 1) ? mm[k / 2].y : mm[k / 2].x;
+        const int gs = (int)((g[k] ^ m) + (m & 0x01010101u));
+#pragma unroll
+        for (int c = 0; c < NC; c++) sumi[c] = dot4(gs, u[c][k], sumi[c]);
+      }
+      const int ls = (int)(aux >> 28);
+      const float d = (r & 1) ? half_hi(w[24 + r / 2]) : half_lo(w[24 + r / 2]);
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const int si = (mul24(ls, sumi[c]) + sumi[c] / 2) / 2;
+        acc[r * NC + c] += (d * dy[c]) * (float)si;
+      }
+    }
+  } else if constexpr (TYPE == kIQ1M) {
+    int sy[NC][4];  // activation sums of the 4 groups of 8 (the delta term multiplies them)
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+      for (int p = 0; p < 4; p++) sy[c][p] = dot4(u[c][2 * p + 1], 0x01010101, dot4(u[c][2 * p], 0x01010101, 0));
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const uint32_t qs = w[r];
+      const uint32_t qh16 = (w[8 + r / 2] >> (16 * (r & 1))) & 0xFFFF;
+      uint32_t grid[4];
+#pragma unroll
+      for (int p = 0; p < 4; p++) grid[p] = lut[((qs >> (8 * p)) & 0xFF) | ((((qh16 >> (4 * p)) & 7)) << 8)];
+      int si[NC][2];
+      float sf[NC][2];
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        si[c][0] = si[c][1] = 0;
+        sf[c][0] = sf[c][1] = 0.0f;
+      }
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int g0 = (int)(grid[p] & 0x0F0F0F0Fu), g1 = (int)((grid[p] >> 4) & 0x0F0F0F0Fu);
+        const float delta = ((qh16 >> (4 * p)) & 8) ? -1.125f : -0.875f;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          si[c][p / 2] = dot4(g1, u[c][2 * p + 1], dot4(g0, u[c][2 * p], si[c][p / 2]));
+          sf[c][p / 2] += delta * (float)sy[c][p];
+        }
+      }
+      const uint32_t sc6 = (w[12 + r / 4] >> (8 * (r & 3))) & 0xFF;
+      const float sc0 = (float)(2 * (int)(sc6 & 7) + 1), sc1 = (float)(2 * (int)((sc6 >> 3) & 7) + 1);
+      const float d = (r & 1) ? half_hi(w[14 + r / 2]) : half_lo(w[14 + r / 2]);
+#pragma unroll
+      for (int c = 0; c < NC; c++)
+        acc[r * NC + c] += (d * dy[c]) * ((((float)si[c][0] + sf[c][0]) * sc0) + (((float)si[c][1] + sf[c][1]) * sc1));
+    }
   }
 }
 
@@ -397,18 +673,30 @@ constexpr int waves_per_tile(int K) {
 template <int TYPE, int NC>
 __global__ void __launch_bounds__(64 * kMaxW) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                     float* __restrict__ y, int K, int W) {
-  __shared__ uint32_t lut[TYPE == kIQ3S ? 1024 : 1];
+  constexpr int LW = LutInfo<TYPE>::words;
+  __shared__ uint32_t lut[LW > 0 ? LW : 1];
   __shared__ float part[kMaxW][8 * NC];
-  if constexpr (TYPE == kIQ3S) {
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) lut[i] = kIQ3SGrid[i];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) {  // sign byte -> byte masks of its low and high nibble
+  if constexpr (LW > 0) {
+    constexpr int G = LutInfo<TYPE>::grid, NM = LutInfo<TYPE>::masks;
+    for (int i = threadIdx.x; i < G; i += blockDim.x) {
+      uint32_t v;
+      if constexpr (TYPE == kIQ3S) v = kIQ3SGrid[i];
+      else if constexpr (TYPE == kIQ3XXS) v = kIQ3XXSGrid[i];
+      else if constexpr (TYPE == kIQ1M) v = kIQ1SGrid[i];
+      else if constexpr (TYPE == kIQ2XXS) v = (uint32_t)(kIQ2XXSGrid[i / 2] >> (32 * (i & 1)));
+      else if constexpr (TYPE == kIQ2XS) v = (uint32_t)(kIQ2XSGrid[i / 2] >> (32 * (i & 1)));
+      else v = (uint32_t)(kIQ2SGrid[i / 2] >> (32 * (i & 1)));
+      lut[i] = v;
+    }
+    for (int i = threadIdx.x; i < NM; i += blockDim.x) {
+      const int sb = NM == 128 ? (i | ((__builtin_popcount(i) & 1) << 7)) : i;  // ksigns: even count of negatives
       uint32_t m0 = 0, m1 = 0;
       for (int j = 0; j < 4; j++) {
-        m0 |= ((i >> j) & 1) ? 0xFFu << (8 * j) : 0u;
-        m1 |= ((i >> (4 + j)) & 1) ? 0xFFu << (8 * j) : 0u;
+        m0 |= ((sb >> j) & 1) ? 0xFFu << (8 * j) : 0u;
+        m1 |= ((sb >> (4 + j)) & 1) ? 0xFFu << (8 * j) : 0u;
       }
-      lut[512 + 2 * i] = m0;
-      lut[513 + 2 * i] = m1;
+      lut[G + 2 * i] = m0;
+      lut[G + 2 * i + 1] = m1;
     }
   }
   uint32_t kv[4] = {0, 0, 0, 0};
@@ -418,7 +706,7 @@ __global__ void __launch_bounds__(64 * kMaxW) qgemv_kernel(Mat m, const int8_t* 
       kv[i] = (uint32_t)(uint8_t)kIQ4NL[4 * i] | ((uint32_t)(uint8_t)kIQ4NL[4 * i + 1] << 8) |
               ((uint32_t)(uint8_t)kIQ4NL[4 * i + 2] << 16) | ((uint32_t)(uint8_t)kIQ4NL[4 * i + 3] << 24);
   }
-  if constexpr (TYPE == kIQ3S) __syncthreads();
+  if constexpr (LW > 0) __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int tile = blockIdx.x;
   const int wv = wave;
@@ -534,12 +822,21 @@ extern "C" int q27h_qmat_repack(int type, int N, int K, const void* raw, void* b
   const dim3 grid((unsigned)((nchunks + 255) / 256));
   const uint8_t* r = (const uint8_t*)raw;
   const int nb = K / 256;
+#define Q27H_REPACK(T) hipLaunchKernelGGL(repack_kernel<T>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], \
+                                           b + off[3], b + off[4], nb, nchunks)
   switch (type) {
-    case kQ4K: hipLaunchKernelGGL(repack_kernel<kQ4K>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
-    case kQ6K: hipLaunchKernelGGL(repack_kernel<kQ6K>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
-    case kIQ3S: hipLaunchKernelGGL(repack_kernel<kIQ3S>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
-    default: hipLaunchKernelGGL(repack_kernel<kIQ4XS>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], b + off[3], b + off[4], nb, nchunks); break;
+    case kQ2K: Q27H_REPACK(kQ2K); break;
+    case kQ4K: Q27H_REPACK(kQ4K); break;
+    case kQ6K: Q27H_REPACK(kQ6K); break;
+    case kIQ2XXS: Q27H_REPACK(kIQ2XXS); break;
+    case kIQ2XS: Q27H_REPACK(kIQ2XS); break;
+    case kIQ3XXS: Q27H_REPACK(kIQ3XXS); break;
+    case kIQ3S: Q27H_REPACK(kIQ3S); break;
+    case kIQ2S: Q27H_REPACK(kIQ2S); break;
+    case kIQ1M: Q27H_REPACK(kIQ1M); break;
+    default: Q27H_REPACK(kIQ4XS); break;
   }
+#undef Q27H_REPACK
   return check_launch("qmat_repack");
 }
 
@@ -558,9 +855,15 @@ extern "C" int q27h_qgemv(int type, int N, int K, const void* buf, const int8_t*
   // three columns run as two launches (columns 0-1, then column 2), each with its own rows of y
   auto run = [&](const int8_t* q, const float* d, float* yy, int nc) {
     switch (type) {
+      case kQ2K: launch_nc<kQ2K>(m, q, d, yy, K, nc, st); break;
       case kQ4K: launch_nc<kQ4K>(m, q, d, yy, K, nc, st); break;
       case kQ6K: launch_nc<kQ6K>(m, q, d, yy, K, nc, st); break;
+      case kIQ2XXS: launch_nc<kIQ2XXS>(m, q, d, yy, K, nc, st); break;
+      case kIQ2XS: launch_nc<kIQ2XS>(m, q, d, yy, K, nc, st); break;
+      case kIQ3XXS: launch_nc<kIQ3XXS>(m, q, d, yy, K, nc, st); break;
       case kIQ3S: launch_nc<kIQ3S>(m, q, d, yy, K, nc, st); break;
+      case kIQ2S: launch_nc<kIQ2S>(m, q, d, yy, K, nc, st); break;
+      case kIQ1M: launch_nc<kIQ1M>(m, q, d, yy, K, nc, st); break;
       default: launch_nc<kIQ4XS>(m, q, d, yy, K, nc, st); break;
     }
   };

@@ -139,8 +139,9 @@ def quantize_q8_1(x, xq, xd, K, ncols, s=None, xs=None):
 
 
 # Weight types of the decode GEMV: ggml type ids (src/gguf.h:12-14).
-Q4_K, Q6_K, IQ3_S, IQ4_XS = 12, 14, 21, 23
-BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, IQ3_S: 110, IQ4_XS: 136}
+Q2_K, Q4_K, Q6_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ1_M = 10, 12, 14, 16, 17, 18, 21, 22, 23, 29
+BLOCK_BYTES = {Q2_K: 84, Q4_K: 144, Q6_K: 210, IQ2_XXS: 66, IQ2_XS: 74, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ4_XS: 136,
+               IQ1_M: 56}
 
 
 class QMat:

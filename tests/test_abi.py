@@ -100,7 +100,7 @@ void decode_gemv(const void* raw, const int8_t* xq, const float* xd, float* y, h
   q27::QMat m = q27::qmat_upload_raw(q27::GType::IQ3_S, 17408, 5120, raw, s);  // src/qmat.h:34 (device half)
   q27::qgemv(m, xq, xd, y, 4, s);                                                // src/qmat.h:44-46
   q27::qmat_free(m);
-  (void)q27::qmat_supported(q27::GType::Q4_K);
+  (void)q27::qmat_supported(q27::GType::IQ1_M);
 }
 ''')
     inc = os.path.join(ROOT, "include")

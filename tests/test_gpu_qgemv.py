@@ -10,7 +10,7 @@ from conftest import assert_bits_equal
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [cd.Q4_K, cd.Q6_K, cd.IQ4_XS, cd.IQ3_S]
+TYPES = cd.QG_TYPES
 
 
 def say(msg):
@@ -77,7 +77,7 @@ def test_qgemv_errors(q27, dev):
 
     raw = torch.zeros(144 * 8, dtype=torch.uint8, device=dev)
     with pytest.raises(Q27Error):
-        q27.ops.qmat_upload(raw, 8, 8, 256)  # Q8_0 is not a GEMV type
+        q27.ops.qmat_upload(raw, 8, 8, 256)  # Q8_0 is not a GEMV type (neither in the reference)
     m = q27.ops.qmat_upload(raw, cd.Q4_K, 8, 256)
     xq = torch.zeros(5 * 256, dtype=torch.int8, device=dev)
     xd = torch.zeros(5 * 8, device=dev)
