@@ -466,6 +466,39 @@ def bench_gemv(q27, torch):
     return out
 
 
+def bench_gdn(q27, torch, M=2048):
+    """The delta-rule recurrence (gdn_step, src/ops.cu:449-572) of one GDN layer at the model's head counts (48
+    value heads on 16 key heads, 128 x 128 f32 state each): prefill of M tokens in flip mode and a decode launch of
+    T = 4 tokens with snapshots (graph-replayed, as in a decode step). GB/s counts the compulsory bytes: state in
+    and out (plus the snapshot planes), q / k per key head, v, g, beta and o per token. The recurrence is serial in
+    the tokens, so its bound is the per-token latency of the update chain, not HBM; us_per_token reports that."""
+    dev = torch.device("cuda:0")
+    H, HK, D = 48, 16, 128
+    stride = 2 * HK * D + H * D
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    out = {}
+    for name, T, flip in (("prefill", M, True), ("decode_T4", 4, False)):
+        x = torch.randn(T * stride, device=dev, generator=g) * 0.088
+        gg = -torch.rand(T * H, device=dev, generator=g) * 0.5
+        beta = torch.rand(T * H, device=dev, generator=g)
+        planes = torch.randn(4 * H * D * D, device=dev, generator=g) * 0.5
+        pin = torch.zeros(1, dtype=torch.int32, device=dev)
+        o = torch.empty(T * H * D, device=dev)
+
+        def fn(i=0):
+            q27.ops.gdn_step(x, x[HK * D:], x[2 * HK * D:], stride, gg, beta, planes, pin, o, H, HK, T, 0.0884, not flip,
+                             flip=flip)
+
+        us = time_back_to_back(torch, fn, 20) if flip else time_graph(torch, fn, 64)
+        state = H * D * D * 4
+        b = state * (1 + (1 if flip else T)) + T * (2 * HK * D + 2 * H * D + 2 * H) * 4
+        out[name] = {"us": round(us, 2), "tokens": T, "us_per_token": round(us / T, 3), "GBps": round(b / us / 1e3, 1),
+                     "MB": round(b / 1e6, 2)}
+        log(f"  gdn_step {name:9s} T={T:5d} {us:8.2f} us ({us / T:.3f} us/token) {b / us / 1e3:7.1f} GB/s")
+    return out
+
+
 def bench_cfg1(q27, torch):
     """RMSNorm -> q8_1 of one 5120 row (0.1% outliers x50) on the CPU oracle and on the GPU, with the
     bit-exact comparison of xq / xd / xs."""
@@ -660,6 +693,7 @@ def main():
     torch.cuda.empty_cache()
     gemv = bench_gemv(q27, torch)
     torch.cuda.empty_cache()
+    gdn_rec = bench_gdn(q27, torch)
 
     if args.calib_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -701,6 +735,7 @@ def main():
         "gathers_cfg4": gathers,
         "multimodal_cfg5": multimodal,
         "decode_gemv": gemv,
+        "gdn_recurrence": gdn_rec,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

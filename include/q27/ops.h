@@ -56,6 +56,13 @@ inline void gdn_conv(const float* x, const float* w, float* planes, const int* i
                      bool snapshots, hipStream_t s) {
   q27h_check(q27h_gdn_conv(x, w, planes, in_plane, y, C, T, snapshots ? 1 : 0, s));
 }
+// src/ops.h:40-45
+inline void gdn_step(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
+                     float* planes, const int* in_plane, float* o, int H, int HK, int T, float scale, bool snapshots,
+                     hipStream_t s, bool flip = false) {
+  q27h_check(q27h_gdn_step(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, snapshots ? 1 : 0, s,
+                           flip ? 1 : 0));
+}
 // src/ops.h:36
 inline void l2norm_heads(float* x, int n, int heads, int T, int stride, float eps, hipStream_t s) {
   q27h_check(q27h_l2norm_heads(x, n, heads, T, stride, eps, s));

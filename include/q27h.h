@@ -87,6 +87,15 @@ int q27h_gdn_gates(const float* a, const float* b, const float* ssm_a, const flo
  * planes [4][C][3]; *in_plane (device) selects the input state. */
 int q27h_gdn_conv(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T, int snapshots,
                   q27h_stream_t s);
+/* gdn_step (src/ops.h:40-45, src/ops.cu:449-572 and 784-793): the gated delta rule over T tokens for H value heads
+ * of 128 x 128 f32 state (value head h uses key head h % HK); q / k / v rows of `stride` floats (q, k at
+ * kh * 128, v at h * 128), g / beta [T][H], o [T][H][128] = (S^T q) * scale. planes [4][H][128 col][128 i].
+ * flip = 0 (decode, T <= 4): read plane *in_plane, write plane t after token t when snapshots, else plane T - 1.
+ * flip = 1 (prefill, any T): the final state goes to plane (*in_plane == 0 ? 1 : 0); no snapshots.
+ * q, k and planes 16-byte aligned, stride % 4 == 0. */
+int q27h_gdn_step(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
+                  float* planes, const int* in_plane, float* o, int H, int HK, int T, float scale, int snapshots,
+                  q27h_stream_t s, int flip);
 /* gdn_conv_l2 (src/ops.h:112-114, src/ops.cu:731-737): gdn_conv + l2norm_heads of the first n_norm_heads heads
  * + gdn_gates in one launch. C % 128 == 0 and C / 128 - n_norm_heads == H. pf/pf_bytes ignored. */
 int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,

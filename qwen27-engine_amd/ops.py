@@ -66,6 +66,12 @@ def gdn_conv(x, w, planes, in_plane, y, C, T, snapshots, s=None):
     check(lib().q27h_gdn_conv(_ptr(x), _ptr(w), _ptr(planes), _ptr(in_plane), _ptr(y), C, T, int(snapshots), _stream(s)))
 
 
+def gdn_step(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, snapshots, s=None, flip=False):
+    """src/ops.h:40-45: the gated delta rule over T tokens (flip: prefill, final state to the other plane)."""
+    check(lib().q27h_gdn_step(_ptr(q), _ptr(k), _ptr(v), stride, _ptr(g), _ptr(beta), _ptr(planes), _ptr(in_plane),
+                              _ptr(o), H, HK, T, scale, int(snapshots), _stream(s), int(flip)))
+
+
 def l2norm_heads(x, n, heads, T, stride, eps, s=None):
     check(lib().q27h_l2norm_heads(_ptr(x), n, heads, T, stride, eps, _stream(s)))
 

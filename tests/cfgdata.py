@@ -129,3 +129,17 @@ def q8_activations(oracle, r, ncols, K, std=1.0):
     x = normal(r, ncols * K, std)
     xq, xd, _ = oracle.quantize_q8_1(x, K, ncols)
     return xq, xd
+
+
+def gdn_inputs(r, T, H=HV, HK=KH, planes_std=0.5):
+    """Inputs of the delta rule as the model feeds them: one conv-output row per token ([q | k | v], stride
+    2 * HK * 128 + H * 128) with q and k of unit norm per head, g = softplus(.) * ssm_a < 0, beta in (0, 1), and
+    four random state planes [4][H][128][128]."""
+    stride = 2 * HK * 128 + H * 128
+    x = normal(r, T * stride).reshape(T, stride)
+    qk = x[:, : 2 * HK * 128].reshape(T, 2 * HK, 128)
+    qk /= np.sqrt((qk.astype(np.float64) ** 2).sum(-1, keepdims=True)).astype(np.float32)
+    g = (-np.abs(r.standard_normal(T * H)) * 0.5 - 0.01).astype(np.float32)
+    beta = (1.0 / (1.0 + np.exp(-r.standard_normal(T * H)))).astype(np.float32)
+    planes = normal(r, 4 * H * 128 * 128, std=planes_std)
+    return x.reshape(-1).copy(), stride, g, beta, planes

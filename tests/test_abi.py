@@ -57,6 +57,11 @@ FAKE = 1 << 20  # an aligned non-null address: the calls below must fail before 
      -1, "T must be <= 4"),
     (lambda o: o.gdn_conv_prefill(FAKE, FAKE, FAKE, FAKE, FAKE, 10200, 64, 32, 1e-6, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 0),
      -1, "bad shape"),
+    (lambda o: o.gdn_step(FAKE, FAKE, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 5, 0.088, True, 0), -1, "T must be <= 4"),
+    (lambda o: o.gdn_step(FAKE, FAKE, FAKE, 10242, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 2048, 0.088, False, 0, True), -1,
+     "bad shape"),
+    (lambda o: o.gdn_step(FAKE, FAKE + 8, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 4, 0.088, True, 0), -4,
+     "alignment"),
     (lambda o: o.get_rows_q4_k(FAKE, 2880, FAKE, 4, FAKE, 5000, 0), -1, "multiple of 256"),
     (lambda o: o.get_rows_q8_0(FAKE, 100, FAKE, 4, FAKE, 5120, 0), -1, "row_bytes"),
     (lambda o: o.rmsnorm_q8(FAKE + 4, FAKE, None, FAKE, FAKE, 5120, 4, 1e-6, 0), -4, "alignment"),
@@ -76,6 +81,7 @@ def test_empty_inputs_are_no_ops(q27):
     q27.ops.gated_rmsnorm_q8(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1e-6, 0)
     q27.ops.get_rows_iq2_s(FAKE, 1640, FAKE, 0, FAKE, 5120, 0)
     q27.ops.attn_prep(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1e-6, 0.6, 24, 4, 16, True, 0)
+    q27.ops.gdn_step(FAKE, FAKE, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 0, 0.088, True, 0)
 
 
 def test_cpp_dropin_header_compiles(tmp_path):
@@ -94,6 +100,8 @@ void step(float* x, const float* part, const float* w, float* h, int8_t* xq, flo
   q27::quantize_q8_1(x, xq, xd, 6144, 2048, s, xs);
   q27::get_rows_iq2_s(emb, 1640, ids, 4, x, 5120, s);
   q27::gdn_flip_plane(plane, s);
+  q27::gdn_step(x, x + 2048, x + 4096, 10240, g, u, h, plane, h, 48, 16, 4, 0.0884f, true, s);         // decode
+  q27::gdn_step(x, x + 2048, x + 4096, 10240, g, u, h, plane, h, 48, 16, 2048, 0.0884f, false, s, true);  // prefill
   (void)q27::kv_cache_bytes(4, 180224, true);
 }
 void decode_gemv(const void* raw, const int8_t* xq, const float* xd, float* y, hipStream_t s) {
