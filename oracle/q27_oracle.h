@@ -69,6 +69,10 @@ void q27o_gdn_conv_prefill(const float* x, const float* w, float* planes, int in
 /* gdn_step (q27_oracle_gdn.c): the delta-rule recurrence of src/ops.h:40-45. */
 int q27o_gdn_step(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
                   float* planes, int in_plane, float* o, int H, int HK, int T, float scale, int snapshots, int flip);
+/* the same with the part count (8 or 16) as an argument */
+int q27o_gdn_step_parts(int parts, const float* q, const float* k, const float* v, int stride, const float* g,
+                        const float* beta, float* planes, int in_plane, float* o, int H, int HK, int T, float scale,
+                        int snapshots, int flip);
 
 /* ---- attention input stage: Q/K RMSNorm + (IM)RoPE + KV-cache write */
 size_t q27o_kv_cache_bytes(int nkvh, int n_ctx, int q8);

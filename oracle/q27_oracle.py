@@ -59,6 +59,7 @@ _SIGS = {
     "q27o_qgemv_waves": (_i, [_i, _i]),
     "q27o_qgemv": (_i, [_i, _p, _i, _i, _p, _p, _p, _i]),
     "q27o_gdn_step": (_i, [_p, _p, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, C.c_float, _i, _i]),
+    "q27o_gdn_step_parts": (_i, [_i, _p, _p, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, C.c_float, _i, _i]),
 }
 
 _lib = None
@@ -321,12 +322,15 @@ def qgemv_waves(N, K):
     return int(lib().q27o_qgemv_waves(N, K))
 
 
-def gdn_step(q, k, v, stride, g, beta, planes, in_plane, H, HK, T, scale, snapshots, flip):
-    """Delta-rule recurrence (q27_oracle_gdn.c). q / k / v share the row stride; returns (o [T][H][128], planes)."""
+def gdn_step(q, k, v, stride, g, beta, planes, in_plane, H, HK, T, scale, snapshots, flip, parts=None):
+    """Delta-rule recurrence (q27_oracle_gdn.c). q / k / v share the row stride; returns (o [T][H][128], planes).
+    `parts` (8 or 16) overrides the contract's part count."""
     q, k, v, g, beta = map(_f32, (q, k, v, g, beta))
     planes = _f32(planes).copy()
     o = np.zeros(T * H * 128, np.float32)
-    if lib().q27o_gdn_step(_ptr(q), _ptr(k), _ptr(v), stride, _ptr(g), _ptr(beta), _ptr(planes), in_plane, _ptr(o), H,
-                           HK, T, scale, int(snapshots), int(flip)) != 0:
+    args = (_ptr(q), _ptr(k), _ptr(v), stride, _ptr(g), _ptr(beta), _ptr(planes), in_plane, _ptr(o), H, HK, T, scale,
+            int(snapshots), int(flip))
+    rc = lib().q27o_gdn_step(*args) if parts is None else lib().q27o_gdn_step_parts(parts, *args)
+    if rc != 0:
         raise ValueError("q27o_gdn_step: bad shape")
     return o, planes

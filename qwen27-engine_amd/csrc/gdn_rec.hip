@@ -10,99 +10,174 @@
 //
 // gfx950 layout: 16 lanes per column, lane part p holds S[8p .. 8p + 7][col] in registers for the whole sequence; a
 // 512-thread workgroup = 32 columns of one head (grid H x 4). Per token each lane forms its 8-term partial dot
-// products as four interleaved partial sums, (k0 + k1) + (k2 + k3), and the 16 parts are added by an xor butterfly
-// (masks 1, 2, 7, 8). q, k of GT tokens (shared by the 32 columns), v, e^g and beta are staged in
-// LDS once per GT tokens. The CPU checker restates this order exactly.
+// products as four interleaved fused multiply-add chains, (k0 + k1) + (k2 + k3), and the 16 parts are added by an
+// xor butterfly (masks 1, 2, 7, 8); the state update is fma(k, delta, e^g S). q, k of kGT tokens (shared by the
+// 32 columns), v, e^g and beta are staged in LDS, double-buffered: the next round's global loads are in flight
+// while the current round's tokens run. The CPU checker restates this order exactly. The kernel is bound by VALU
+// issue (about 60 instructions per token and wave, two waves per SIMD), not by HBM.
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
 namespace q27h {
 namespace {
 
-constexpr int kParts = 16, kEpl = 128 / kParts;  // lanes per column, state elements per lane
-constexpr int kCols = 32;                         // columns per workgroup
-constexpr int kGT = 32;                           // tokens staged per LDS round
+#ifndef Q27H_GDN_PARTS
+#define Q27H_GDN_PARTS 16  // 8 parts of 16 (one wave per SIMD) measured 616 us vs 574 us at 2048 tokens
+#endif
+constexpr int kParts = Q27H_GDN_PARTS;  // lanes per column
+constexpr int kCols = 32;               // columns per workgroup
+constexpr int kGT = 32;                 // tokens staged per LDS round
 
-// Sum over the 16 parts of a column (lanes 16c .. 16c + 15): xor butterfly with masks 1, 2, 7, 8, which span lane
-// bits 0..3 and are all DPP moves (quad_perm, row_half_mirror, row_ror:8). Each step adds a lane pair's two values,
-// so every part ends with the bit-identical sum.
+// Sum over the parts of a column (PARTS consecutive lanes): xor butterfly with masks 1, 2, 7 (, 8), which span the
+// lane bits of a part index and are all DPP moves (quad_perm, row_half_mirror, row_ror:8). Each step adds a lane
+// pair's two values, so every part ends with the bit-identical sum.
+template <int PARTS>
 __device__ __forceinline__ float parts_sum(float v) {
   v += lane_xor<1>(v);
   v += lane_xor<2>(v);
   v += lane_xor<7>(v);
-  v += lane_xor<8>(v);
+  if constexpr (PARTS == 16) v += lane_xor<8>(v);
   return v;
 }
 
-__global__ void __launch_bounds__(kCols * kParts) gdn_rec_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                                 const float* __restrict__ v, int stride,
-                                                                 const float* __restrict__ g, const float* __restrict__ beta,
-                                                                 float* __restrict__ planes, const int* __restrict__ in_plane,
-                                                                 float* __restrict__ o, int H, int HK, int T, float scale,
-                                                                 int snapshots, int flip) {
-  __shared__ __align__(16) float sq[kGT][128];
-  __shared__ __align__(16) float sk[kGT][128];
-  __shared__ float sv[kGT][kCols];
-  __shared__ float sg[kGT], sb[kGT];
+// One staging round in registers: q / k of kGT tokens as float4 pieces (32 per token and vector), v of the
+// workgroup's kCols columns, g and beta.
+template <int THREADS>
+struct Stage {
+  static constexpr int NQ = kGT * 32 / THREADS, NV = kGT * kCols / THREADS;
+  float4 q[NQ], k[NQ];
+  float v[NV];
+  float g, b;
+};
+
+#ifndef Q27H_GDN_UNROLL
+#define Q27H_GDN_UNROLL 32  // full rounds fully unrolled: 509 us for 2048 tokens, 535 us with 1, 544 us with 4
+#endif
+
+// SNAP: decode with per-token snapshots (plane t after token t); otherwise only the final state is written.
+template <int PARTS, bool SNAP>
+__global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                                const float* __restrict__ v, int stride,
+                                                                const float* __restrict__ g, const float* __restrict__ beta,
+                                                                float* __restrict__ planes, const int* __restrict__ in_plane,
+                                                                float* __restrict__ o, int H, int HK, int T, float scale,
+                                                                int flip) {
+  constexpr int EPL = 128 / PARTS, PAD = EPL + 4, ROW = PARTS * PAD, THREADS = kCols * PARTS;
+  // q / k rows padded by 4 floats per part (the parts' float4 reads fall in different banks); two buffers, the
+  // next round is loaded while the current one is consumed
+  __shared__ __align__(16) float sq[2][kGT][ROW];
+  __shared__ __align__(16) float sk[2][kGT][ROW];
+  __shared__ float sv[2][kGT][kCols];
+  __shared__ float sg[2][kGT], sb[2][kGT];
   const int h = blockIdx.x, kh = h % HK;
-  const int tid = threadIdx.x, p = tid & (kParts - 1), cl = tid / kParts, col = blockIdx.y * kCols + cl;
+  const int tid = threadIdx.x, p = tid & (PARTS - 1), cl = tid / PARTS, col = blockIdx.y * kCols + cl;
   const size_t plane_sz = (size_t)H * 128 * 128;
   const int pin = *in_plane;
-  const size_t soff = ((size_t)h * 128 + col) * 128 + kEpl * p;
-  float s[kEpl];
+  const size_t soff = ((size_t)h * 128 + col) * 128 + EPL * p;
+  float s[EPL];
   {
     const float* src = planes + (size_t)pin * plane_sz + soff;
-    const float4 a = ld4(src), b = ld4(src + 4);
-    s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w; s[4] = b.x; s[5] = b.y; s[6] = b.z; s[7] = b.w;
-  }
-  const int out_plane = flip ? (pin == 0 ? 1 : 0) : T - 1;
-  for (int t0 = 0; t0 < T; t0 += kGT) {
-    const int nt = min(kGT, T - t0);
-    __syncthreads();  // the previous round's reads of the staging buffers are done
-    for (int i = tid; i < nt * 32; i += kCols * kParts) {  // 32 float4 per token per vector
-      const int t = i >> 5, e4 = (i & 31) * 4;
-      *(float4*)&sq[t][e4] = ld4(q + (size_t)(t0 + t) * stride + kh * 128 + e4);
-      *(float4*)&sk[t][e4] = ld4(k + (size_t)(t0 + t) * stride + kh * 128 + e4);
+#pragma unroll
+    for (int i = 0; i < EPL; i += 4) {
+      const float4 a = ld4(src + i);
+      s[i] = a.x; s[i + 1] = a.y; s[i + 2] = a.z; s[i + 3] = a.w;
     }
-    for (int i = tid; i < nt * kCols; i += kCols * kParts) {
-      const int t = i / kCols, c = i % kCols;
-      sv[t][c] = v[(size_t)(t0 + t) * stride + h * 128 + blockIdx.y * kCols + c];
+  }
+  using St = Stage<THREADS>;
+  auto load = [&](St& r, int t0) {
+    const int nt = min(kGT, T - t0);
+#pragma unroll
+    for (int j = 0; j < St::NQ; j++) {
+      const int i = tid + j * THREADS, t = i >> 5, e4 = (i & 31) * 4;
+      if (t < nt) {
+        r.q[j] = ld4(q + (size_t)(t0 + t) * stride + kh * 128 + e4);
+        r.k[j] = ld4(k + (size_t)(t0 + t) * stride + kh * 128 + e4);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < St::NV; j++) {
+      const int i = tid + j * THREADS, t = i / kCols, c = i % kCols;
+      if (t < nt) r.v[j] = v[(size_t)(t0 + t) * stride + h * 128 + blockIdx.y * kCols + c];
     }
     if (tid < nt) {
-      sg[tid] = q27_expf(g[(size_t)(t0 + tid) * H + h]);
-      sb[tid] = beta[(size_t)(t0 + tid) * H + h];
+      r.g = g[(size_t)(t0 + tid) * H + h];
+      r.b = beta[(size_t)(t0 + tid) * H + h];
     }
-    __syncthreads();
-    for (int tt = 0; tt < nt; tt++) {
-      const float4 k0 = *(const float4*)&sk[tt][kEpl * p], k1 = *(const float4*)&sk[tt][kEpl * p + 4];
-      const float4 q0 = *(const float4*)&sq[tt][kEpl * p], q1 = *(const float4*)&sq[tt][kEpl * p + 4];
-      const float kr[kEpl] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      const float qr[kEpl] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  };
+  auto store = [&](const St& r, int buf, int t0) {
+    const int nt = min(kGT, T - t0);
+#pragma unroll
+    for (int j = 0; j < St::NQ; j++) {
+      const int i = tid + j * THREADS, t = i >> 5, e4 = (i & 31) * 4, pe = (e4 / EPL) * PAD + e4 % EPL;
+      if (t < nt) {
+        *(float4*)&sq[buf][t][pe] = r.q[j];
+        *(float4*)&sk[buf][t][pe] = r.k[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < St::NV; j++) {
+      const int i = tid + j * THREADS, t = i / kCols, c = i % kCols;
+      if (t < nt) sv[buf][t][c] = r.v[j];
+    }
+    if (tid < nt) {
+      sg[buf][tid] = q27_expf(r.g);
+      sb[buf][tid] = r.b;
+    }
+  };
+  const int out_plane = flip ? (pin == 0 ? 1 : 0) : T - 1;
+  {
+    St r;
+    load(r, 0);
+    store(r, 0, 0);
+  }
+  __syncthreads();
+  for (int t0 = 0, buf = 0; t0 < T; t0 += kGT, buf ^= 1) {
+    const int nt = min(kGT, T - t0);
+    const bool more = t0 + kGT < T;
+    St r;
+    if (more) load(r, t0 + kGT);  // in flight during the tokens below
+    auto step = [&](int tt) {
+      float kr[EPL], qr[EPL];
+#pragma unroll
+      for (int i = 0; i < EPL; i += 4) {
+        const float4 k4 = *(const float4*)&sk[buf][tt][p * PAD + i];
+        const float4 q4 = *(const float4*)&sq[buf][tt][p * PAD + i];
+        kr[i] = k4.x; kr[i + 1] = k4.y; kr[i + 2] = k4.z; kr[i + 3] = k4.w;
+        qr[i] = q4.x; qr[i + 1] = q4.y; qr[i + 2] = q4.z; qr[i + 3] = q4.w;
+      }
       float kq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < kEpl; i++) kq[i & 3] += s[i] * kr[i];
-      const float kv = parts_sum((kq[0] + kq[1]) + (kq[2] + kq[3]));
-      const float gv = sg[tt];
-      const float delta = (sv[tt][cl] - gv * kv) * sb[tt];
+      for (int i = 0; i < EPL; i++) kq[i & 3] = __builtin_fmaf(s[i], kr[i], kq[i & 3]);
+      const float kv = parts_sum<PARTS>((kq[0] + kq[1]) + (kq[2] + kq[3]));
+      const float gv = sg[buf][tt];
+      const float delta = (sv[buf][tt][cl] - gv * kv) * sb[buf][tt];
       float aq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < kEpl; i++) {
-        s[i] = gv * s[i] + kr[i] * delta;
-        aq[i & 3] += s[i] * qr[i];
+      for (int i = 0; i < EPL; i++) {
+        s[i] = __builtin_fmaf(kr[i], delta, gv * s[i]);
+        aq[i & 3] = __builtin_fmaf(s[i], qr[i], aq[i & 3]);
       }
-      const float at = parts_sum((aq[0] + aq[1]) + (aq[2] + aq[3]));
+      const float at = parts_sum<PARTS>((aq[0] + aq[1]) + (aq[2] + aq[3]));
       const int t = t0 + tt;
       if (p == 0) o[((size_t)t * H + h) * 128 + col] = at * scale;
-      if (!flip && snapshots && t < T - 1) {
+      if (SNAP && t < T - 1) {
         float* W = planes + (size_t)t * plane_sz + soff;
-        st4(W, s[0], s[1], s[2], s[3]);
-        st4(W + 4, s[4], s[5], s[6], s[7]);
+#pragma unroll
+        for (int i = 0; i < EPL; i += 4) st4(W + i, s[i], s[i + 1], s[i + 2], s[i + 3]);
       }
+    };
+    if (nt == kGT) {
+#pragma unroll Q27H_GDN_UNROLL
+      for (int tt = 0; tt < kGT; tt++) step(tt);
+    } else {
+      for (int tt = 0; tt < nt; tt++) step(tt);
     }
+    if (more) store(r, buf ^ 1, t0 + kGT);
+    __syncthreads();
   }
   float* W = planes + (size_t)out_plane * plane_sz + soff;
-  st4(W, s[0], s[1], s[2], s[3]);
-  st4(W + 4, s[4], s[5], s[6], s[7]);
+#pragma unroll
+  for (int i = 0; i < EPL; i += 4) st4(W + i, s[i], s[i + 1], s[i + 2], s[i + 3]);
 }
 
 }  // namespace
@@ -119,7 +194,11 @@ extern "C" int q27h_gdn_step(const float* q, const float* k, const float* v, int
   if (!q || !k || !v || !g || !beta || !planes || !in_plane || !o) return fail(Q27H_ERR_ARG, "gdn_step: null pointer");
   if (!aligned16(q) || !aligned16(k) || !aligned16(planes))
     return fail(Q27H_ERR_ARG, "gdn_step: q, k and planes need 16-byte alignment");
-  hipLaunchKernelGGL(gdn_rec_kernel, dim3(H, 128 / kCols), dim3(kCols * kParts), 0, stream_of(s), q, k, v, stride, g, beta,
-                     planes, in_plane, o, H, HK, T, scale, snapshots, flip);
+  if (!flip && snapshots && T > 1)
+    hipLaunchKernelGGL((gdn_rec_kernel<kParts, true>), dim3(H, 128 / kCols), dim3(kCols * kParts), 0, stream_of(s), q, k,
+                       v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, 0);
+  else
+    hipLaunchKernelGGL((gdn_rec_kernel<kParts, false>), dim3(H, 128 / kCols), dim3(kCols * kParts), 0, stream_of(s), q, k,
+                       v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, flip);
   return check_launch("gdn_step");
 }
