@@ -499,6 +499,56 @@ def bench_gdn(q27, torch, M=2048):
     return out
 
 
+def bench_upload(q27, torch, gib=1.0):
+    """Weight upload from a GGUF file (the reader of src/gguf.cpp and the transfer of src/qmat.h:34): a file of
+    IQ3_S matrices (17408 x 5120 each) written to a temporary directory and mapped, then every tensor copied to HBM
+    (a) with q27h_gguf_upload_rows (pread by 8 threads into pinned staging buffers, DMA overlapped), (b) with
+    q27h_copy_h2d_staged from the mapping, and (c) as the reference does it, one host-to-device copy from the
+    pageable mapping (torch's copy_ of the mapped bytes). Both read the file from the
+    page cache (it was just written). Best of 3 passes, GB/s of file bytes."""
+    import tempfile
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
+    import gguf_writer as W
+
+    dev = torch.device("cuda:0")
+    N, K = 17408, 5120
+    tb = N * K // 256 * 110
+    count = max(1, int(gib * (1 << 30) // tb))
+    r = np.random.default_rng(3)
+    blob = r.integers(0, 256, tb, dtype=np.uint8).tobytes()
+    out = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "w.gguf")
+        with open(path, "wb") as f:
+            f.write(W.build([("general.architecture", W.STR, "qwen35")],
+                            [(f"blk.{i}.ffn_up.weight", 21, (K, N), blob) for i in range(count)]))
+        t0 = time.perf_counter()
+        g = q27.gguf.GGUF(path)
+        parse_ms = (time.perf_counter() - t0) * 1e3
+        ts = g.tensors()
+        dst = torch.empty(tb, dtype=torch.uint8, device=dev)
+        total = tb * count
+        for name, fn in (("staged_pread", lambda t: q27.gguf.upload_rows(t, dst, threads=8)),
+                         ("staged_from_mapping", lambda t: q27.gguf.copy_h2d_staged(dst, t.data, t.nbytes, threads=8)),
+                         ("pageable_copy", lambda t: dst.copy_(torch.from_numpy(t.array()), non_blocking=False))):
+            best = 1e9
+            for _ in range(3):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for t in ts:
+                    fn(t)
+                torch.cuda.synchronize()
+                best = min(best, time.perf_counter() - t0)
+            out[name] = {"GBps": round(total / best / 1e9, 2), "s": round(best, 3)}
+            log(f"  upload {name:14s} {total / 1e9:.2f} GB in {best * 1e3:.0f} ms: {total / best / 1e9:.2f} GB/s")
+        g.close()
+    out.update({"file_GB": round(total / 1e9, 2), "tensors": count, "parse_ms": round(parse_ms, 3)})
+    return out
+
+
 def bench_cfg1(q27, torch):
     """RMSNorm -> q8_1 of one 5120 row (0.1% outliers x50) on the CPU oracle and on the GPU, with the
     bit-exact comparison of xq / xd / xs."""
@@ -694,6 +744,7 @@ def main():
     gemv = bench_gemv(q27, torch)
     torch.cuda.empty_cache()
     gdn_rec = bench_gdn(q27, torch)
+    upload = bench_upload(q27, torch)
 
     if args.calib_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -736,6 +787,7 @@ def main():
         "multimodal_cfg5": multimodal,
         "decode_gemv": gemv,
         "gdn_recurrence": gdn_rec,
+        "gguf_upload": upload,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

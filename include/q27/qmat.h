@@ -5,8 +5,7 @@
 // Weight types of qgemv: the ten of the reference (Q2_K, Q4_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_XS,
 // IQ1_M; q27h_qmat_bytes returns 0 for the others). The prefill
 // GEMM (qgemm) and qmat_upload_shard (the two-GPU split) of the reference are not part of this library.
-// GType / GTensor come from the engine's own gguf.h when it is on the include path; otherwise this header declares
-// the ggml type ids it needs and only the raw-rows upload is available.
+// GType / GTensor come from the drop-in q27/gguf.h (the reference's src/gguf.h).
 #pragma once
 #include <hip/hip_runtime_api.h>
 
@@ -15,21 +14,8 @@
 #include <stdexcept>
 #include <string>
 
-#include "ops.h"
-
-#if __has_include("gguf.h")
 #include "gguf.h"
-#define Q27H_HAVE_GGUF 1
-#else
-namespace q27 {
-// ggml type ids (src/gguf.h:12-14)
-enum class GType : uint32_t {
-  F32 = 0, F16 = 1, Q2_K = 10, Q4_K = 12, Q6_K = 14, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18,
-  IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, IQ1_M = 29, BF16 = 30,
-};
-}  // namespace q27
-#define Q27H_HAVE_GGUF 0
-#endif
+#include "ops.h"
 
 namespace q27 {
 
@@ -77,16 +63,16 @@ inline QMat qmat_upload_raw(GType type, int N, int K, const void* raw_dev, hipSt
   return m;
 }
 
-#if Q27H_HAVE_GGUF
 // src/qmat.h:34: upload rows [row0, row0 + N) of a GGUF tensor through `scratch` (device, >= N row_bytes) and repack.
+// The host -> device transfer is q27h_copy_h2d_staged (pinned staging, several copy threads) instead of one
+// cudaMemcpyAsync from the pageable mapping.
 inline QMat qmat_upload(const GTensor& t, int row0, int N, void* scratch, size_t scratch_bytes, hipStream_t s) {
+  if (row0 < 0 || N < 0 || row0 + N > t.rows()) throw std::runtime_error("qmat: rows outside " + t.name);
   const size_t raw_bytes = (size_t)N * (size_t)t.row_bytes();
   if (raw_bytes > scratch_bytes) throw std::runtime_error("qmat: scratch too small for " + t.name);
-  if (hipMemcpyAsync(scratch, t.data + (size_t)row0 * t.row_bytes(), raw_bytes, hipMemcpyHostToDevice, s) != hipSuccess)
-    throw std::runtime_error("qmat: host-to-device copy failed for " + t.name);
+  q27h_check(q27h_copy_h2d_staged(scratch, t.data + (size_t)row0 * t.row_bytes(), raw_bytes, 0, s));
   return qmat_upload_raw(t.type, N, (int)t.ne[0], scratch, s);
 }
-#endif
 
 // src/qmat.h:41
 inline void qmat_free(QMat& m) {

@@ -30,6 +30,9 @@ extern "C" {
 #define Q27H_ERR_UNSUPPORTED (-2) /* a feature outside this build: the two-GPU exchange arguments */
 #define Q27H_ERR_HIP (-3)         /* a HIP runtime error at launch */
 #define Q27H_ERR_ARG (-4)         /* null or misaligned pointer */
+#define Q27H_ERR_FORMAT (-5)      /* a malformed or unsupported GGUF file (std::runtime_error in the reference) */
+#define Q27H_ERR_IO (-6)          /* a file that cannot be opened or mapped */
+#define Q27H_ERR_NOT_FOUND (-7)   /* a missing GGUF key or tensor */
 
 typedef void* q27h_stream_t;
 
@@ -158,6 +161,73 @@ int q27h_qgemv(int type, int N, int K, const void* buf, const int8_t* xq, const 
                q27h_stream_t s);
 /* Waves that share one 8-row tile in q27h_qgemv (1, 2 or 4): part of the summation order, a function of N only. */
 int q27h_qgemv_waves(int N, int K);
+
+/* ---------------------------------------------------------------- GGUF reader (src/gguf.h, src/gguf.cpp)
+ * Version-3 files only, memory-mapped read-only for the life of the handle; tensor data pointers point into the
+ * mapping (host memory). Errors: Q27H_ERR_IO (cannot open / map), Q27H_ERR_FORMAT with the reference's messages
+ * ("not a GGUF file: ...", "GGUF version N not supported", "gguf: truncated file", "bad n_dims for ...",
+ * "unknown ggml type N", "tensor out of file: ..."), Q27H_ERR_NOT_FOUND for a missing key or tensor. */
+typedef struct q27h_gguf q27h_gguf;
+/* GValue::Kind (src/gguf.h:33-41) */
+#define Q27H_GV_INT 0
+#define Q27H_GV_FLOAT 1
+#define Q27H_GV_BOOL 2
+#define Q27H_GV_STRING 3
+#define Q27H_GV_ARR_INT 4
+#define Q27H_GV_ARR_FLOAT 5
+#define Q27H_GV_ARR_STRING 6
+/* GTensor (src/gguf.h:21-30); name is NUL-terminated and owned by the handle. */
+typedef struct {
+  const char* name;
+  size_t name_len;
+  int type;
+  int n_dims;
+  int64_t ne[4];
+  uint64_t offset;
+  uint64_t nbytes;
+  const uint8_t* data;
+} q27h_gtensor;
+/* GValue (src/gguf.h:33-41): scalars in i / f / s; arrays of n elements in ai / af (owned by the handle) or, for
+ * strings, through q27h_gguf_kv_str_at. */
+typedef struct {
+  int kind;
+  int64_t i;
+  double f;
+  const char* s;
+  size_t s_len;
+  uint64_t n;
+  const int64_t* ai;
+  const double* af;
+} q27h_gvalue;
+/* gtype_block_bytes / gtype_block_size / gtype_name (src/gguf.h:15-19, src/gguf.cpp:18-62); 0 / "?" for a type
+ * the engine does not know (the reference throws). */
+int q27h_gtype_block_bytes(int type);
+int q27h_gtype_block_size(int type);
+const char* q27h_gtype_name(int type);
+/* GGUF::GGUF(path) / ~GGUF (src/gguf.h:46-47, src/gguf.cpp:113-194) */
+int q27h_gguf_open(const char* path, q27h_gguf** out);
+void q27h_gguf_close(q27h_gguf* g);
+/* GGUF::tensors() / find() / tensor() (src/gguf.h:52-54): the index of `name` or -1; entry i (file order). */
+int64_t q27h_gguf_n_tensors(const q27h_gguf* g);
+int64_t q27h_gguf_find(const q27h_gguf* g, const char* name);
+int q27h_gguf_tensor(const q27h_gguf* g, int64_t i, q27h_gtensor* out);
+/* GGUF::has() / kv() (src/gguf.h:56-57); keys in file order for listing. */
+int64_t q27h_gguf_n_kv(const q27h_gguf* g);
+const char* q27h_gguf_key(const q27h_gguf* g, int64_t i);
+int q27h_gguf_kv(const q27h_gguf* g, const char* key, q27h_gvalue* out);
+int q27h_gguf_kv_str_at(const q27h_gguf* g, const char* key, uint64_t j, const char** s, size_t* len);
+
+/* Staged host -> device copy, the transfer of qmat_upload (src/qmat.h:34, which issues one cudaMemcpyAsync from
+ * the pageable mapping): `bytes` from host `src` (e.g. a tensor's data in the mapping) to device `dst` on stream s,
+ * in 16 MiB chunks that `threads` host threads (<= 0: up to 8) copy into six pinned staging buffers while the
+ * previous chunks' DMA runs. Returns once the last DMA is enqueued; src may be reused at once. One call at a time per
+ * process (internally serialised). */
+int q27h_copy_h2d_staged(void* dst, const void* src, size_t bytes, int threads, q27h_stream_t s);
+/* The same transfer for rows [row0, row0 + nrows) of tensor `tensor` of an open file, read with pread from the
+ * file into the staging buffers (no page faults on the mapping): the upload path of qmat_upload when the caller
+ * holds the GGUF. Q27H_ERR_SHAPE for rows outside the tensor, Q27H_ERR_IO if the file cannot be read. */
+int q27h_gguf_upload_rows(const q27h_gguf* g, int64_t tensor, int64_t row0, int64_t nrows, void* dst, int threads,
+                          q27h_stream_t s);
 
 #ifdef __cplusplus
 }

@@ -8,4 +8,4 @@ launch fails, the call raises. The directory name has a hyphen, so load it by pa
                                                   submodule_search_locations=["<repo>/qwen27-engine_amd"])
 """
 from ._lib import LIB_PATH, Q27Error, build_library, lib  # noqa: F401
-from . import ops  # noqa: F401
+from . import gguf, ops  # noqa: F401

@@ -19,6 +19,19 @@ class Q27Error(RuntimeError):
 
 _p, _i, _f, _sz, _i64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_int64
 
+
+class GTensorC(C.Structure):
+    """q27h_gtensor"""
+    _fields_ = [("name", C.c_char_p), ("name_len", C.c_size_t), ("type", C.c_int), ("n_dims", C.c_int),
+                ("ne", C.c_int64 * 4), ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("data", C.c_void_p)]
+
+
+class GValueC(C.Structure):
+    """q27h_gvalue"""
+    _fields_ = [("kind", C.c_int), ("i", C.c_int64), ("f", C.c_double), ("s", C.c_void_p), ("s_len", C.c_size_t),
+                ("n", C.c_uint64), ("ai", C.POINTER(C.c_int64)), ("af", C.POINTER(C.c_double))]
+
+
 # name -> argument types (all return int status unless listed in _RESTYPE)
 SIGNATURES = {
     "q27h_rmsnorm": [_p, _p, _p, _i, _i, _f, _p, _i],
@@ -51,10 +64,26 @@ SIGNATURES = {
     "q27h_qmat_repack": [_i, _i, _i, _p, _p, _p],
     "q27h_qgemv": [_i, _i, _i, _p, _p, _p, _p, _i, _p],
     "q27h_qgemv_waves": [_i, _i],
+    "q27h_gtype_block_bytes": [_i],
+    "q27h_gtype_block_size": [_i],
+    "q27h_gtype_name": [_i],
+    "q27h_gguf_open": [C.c_char_p, C.POINTER(_p)],
+    "q27h_gguf_close": [_p],
+    "q27h_gguf_n_tensors": [_p],
+    "q27h_gguf_find": [_p, C.c_char_p],
+    "q27h_gguf_tensor": [_p, _i64, C.POINTER(GTensorC)],
+    "q27h_gguf_n_kv": [_p],
+    "q27h_gguf_key": [_p, _i64],
+    "q27h_gguf_kv": [_p, C.c_char_p, C.POINTER(GValueC)],
+    "q27h_gguf_kv_str_at": [_p, C.c_char_p, C.c_uint64, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)],
+    "q27h_copy_h2d_staged": [_p, _p, _sz, _i, _p],
+    "q27h_gguf_upload_rows": [_p, _i64, _i64, _i64, _p, _i, _p],
     "q27h_last_error": [],
     "q27h_abi_version": [],
 }
-_RESTYPE = {"q27h_kv_cache_bytes": _sz, "q27h_qmat_bytes": _sz, "q27h_last_error": C.c_char_p}
+_RESTYPE = {"q27h_kv_cache_bytes": _sz, "q27h_qmat_bytes": _sz, "q27h_last_error": C.c_char_p,
+            "q27h_gtype_name": C.c_char_p, "q27h_gguf_close": None, "q27h_gguf_n_tensors": _i64, "q27h_gguf_find": _i64,
+            "q27h_gguf_n_kv": _i64, "q27h_gguf_key": C.c_char_p}
 
 _lib = None
 

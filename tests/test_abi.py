@@ -110,6 +110,16 @@ void decode_gemv(const void* raw, const int8_t* xq, const float* xd, float* y, h
   q27::qmat_free(m);
   (void)q27::qmat_supported(q27::GType::IQ1_M);
 }
+void load_gguf(const char* path, void* scratch, size_t scratch_bytes, hipStream_t s) {
+  q27::GGUF g(path);                                                   // src/gguf.h:46
+  const q27::GTensor& t = g.tensor("blk.0.ffn_up.weight");
+  q27::QMat m = q27::qmat_upload(t, 0, (int)t.ne[1], scratch, scratch_bytes, s);  // src/qmat.h:34
+  (void)g.get_int("qwen35.block_count");
+  (void)g.get_float("qwen35.rope.freq_base");
+  (void)g.get_str("general.architecture");
+  (void)q27::gtype_name(t.type);
+  q27::qmat_free(m);
+}
 ''')
     inc = os.path.join(ROOT, "include")
     r = subprocess.run(["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{inc}", "-I/opt/rocm/include",
