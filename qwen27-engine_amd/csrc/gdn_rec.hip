@@ -25,8 +25,14 @@ namespace {
 #define Q27H_GDN_PARTS 16  // 8 parts of 16 (one wave per SIMD) measured 616 us vs 574 us at 2048 tokens
 #endif
 constexpr int kParts = Q27H_GDN_PARTS;  // lanes per column
-constexpr int kCols = 32;               // columns per workgroup
-constexpr int kGT = 32;                 // tokens staged per LDS round
+#ifndef Q27H_GDN_COLS
+#define Q27H_GDN_COLS 32
+#endif
+constexpr int kCols = Q27H_GDN_COLS;    // columns per workgroup
+#ifndef Q27H_GDN_GT
+#define Q27H_GDN_GT 32
+#endif
+constexpr int kGT = Q27H_GDN_GT;        // tokens staged per LDS round
 
 // Sum over the parts of a column (PARTS consecutive lanes): xor butterfly with masks 1, 2, 7 (, 8), which span the
 // lane bits of a part index and are all DPP moves (quad_perm, row_half_mirror, row_ror:8). Each step adds a lane
