@@ -59,6 +59,20 @@ class GGUF {
  public:
   explicit GGUF(const std::string& path) : path_(path) {
     if (q27h_gguf_open(path.c_str(), &h_) != Q27H_OK) throw std::runtime_error(q27h_last_error());
+    try {
+      load();
+    } catch (...) {
+      q27h_gguf_close(h_);  // the destructor does not run for a constructor that throws
+      throw;
+    }
+  }
+  ~GGUF() { q27h_gguf_close(h_); }
+  GGUF(const GGUF&) = delete;
+  GGUF& operator=(const GGUF&) = delete;
+
+ private:
+  // Copies the tensor directory and the key / value table out of the handle.
+  void load() {
     const int64_t nt = q27h_gguf_n_tensors(h_);
     tensors_.reserve((size_t)nt);
     for (int64_t i = 0; i < nt; i++) {
@@ -77,9 +91,11 @@ class GGUF {
     }
     const int64_t nk = q27h_gguf_n_kv(h_);
     for (int64_t i = 0; i < nk; i++) {
-      const char* key = q27h_gguf_key(h_, i);
+      const char* kp = nullptr;
+      size_t kn = 0;
       q27h_gvalue c;
-      if (q27h_gguf_kv(h_, key, &c) != Q27H_OK) throw std::runtime_error(q27h_last_error());
+      if (q27h_gguf_key(h_, i, &kp, &kn) != Q27H_OK || q27h_gguf_kv_at(h_, i, &c) != Q27H_OK)
+        throw std::runtime_error(q27h_last_error());
       GValue v;
       v.kind = (GValue::Kind)c.kind;
       v.i = c.i;
@@ -92,17 +108,15 @@ class GGUF {
         for (uint64_t j = 0; j < c.n; j++) {
           const char* s = nullptr;
           size_t n = 0;
-          if (q27h_gguf_kv_str_at(h_, key, j, &s, &n) != Q27H_OK) throw std::runtime_error(q27h_last_error());
+          if (q27h_gguf_kv_str_at(h_, i, j, &s, &n) != Q27H_OK) throw std::runtime_error(q27h_last_error());
           v.as.emplace_back(s, n);
         }
       }
-      kv_[key] = std::move(v);
+      kv_[std::string(kp, kn)] = std::move(v);
     }
   }
-  ~GGUF() { q27h_gguf_close(h_); }
-  GGUF(const GGUF&) = delete;
-  GGUF& operator=(const GGUF&) = delete;
 
+ public:
   const GTensor& tensor(const std::string& name) const {
     const GTensor* t = find(name);
     if (!t) throw std::runtime_error("missing tensor " + name);

@@ -211,11 +211,14 @@ void q27h_gguf_close(q27h_gguf* g);
 int64_t q27h_gguf_n_tensors(const q27h_gguf* g);
 int64_t q27h_gguf_find(const q27h_gguf* g, const char* name);
 int q27h_gguf_tensor(const q27h_gguf* g, int64_t i, q27h_gtensor* out);
-/* GGUF::has() / kv() (src/gguf.h:56-57); keys in file order for listing. */
+/* GGUF::has() / kv() (src/gguf.h:56-57). Keys are listed by index in file order; a key is returned as pointer +
+ * length (it may hold any byte, NUL included, as the reference's std::string keys may), and q27h_gguf_kv_at /
+ * q27h_gguf_kv_str_at address a key by that index. q27h_gguf_kv looks a NUL-terminated key up by name. */
 int64_t q27h_gguf_n_kv(const q27h_gguf* g);
-const char* q27h_gguf_key(const q27h_gguf* g, int64_t i);
+int q27h_gguf_key(const q27h_gguf* g, int64_t i, const char** s, size_t* len);
 int q27h_gguf_kv(const q27h_gguf* g, const char* key, q27h_gvalue* out);
-int q27h_gguf_kv_str_at(const q27h_gguf* g, const char* key, uint64_t j, const char** s, size_t* len);
+int q27h_gguf_kv_at(const q27h_gguf* g, int64_t i, q27h_gvalue* out);
+int q27h_gguf_kv_str_at(const q27h_gguf* g, int64_t i, uint64_t j, const char** s, size_t* len);
 
 /* Staged host -> device copy, the transfer of qmat_upload (src/qmat.h:34, which issues one cudaMemcpyAsync from
  * the pageable mapping): `bytes` from host `src` (e.g. a tensor's data in the mapping) to device `dst` on stream s,

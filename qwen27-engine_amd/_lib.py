@@ -73,9 +73,10 @@ SIGNATURES = {
     "q27h_gguf_find": [_p, C.c_char_p],
     "q27h_gguf_tensor": [_p, _i64, C.POINTER(GTensorC)],
     "q27h_gguf_n_kv": [_p],
-    "q27h_gguf_key": [_p, _i64],
+    "q27h_gguf_key": [_p, _i64, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)],
     "q27h_gguf_kv": [_p, C.c_char_p, C.POINTER(GValueC)],
-    "q27h_gguf_kv_str_at": [_p, C.c_char_p, C.c_uint64, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)],
+    "q27h_gguf_kv_at": [_p, _i64, C.POINTER(GValueC)],
+    "q27h_gguf_kv_str_at": [_p, _i64, C.c_uint64, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)],
     "q27h_copy_h2d_staged": [_p, _p, _sz, _i, _p],
     "q27h_gguf_upload_rows": [_p, _i64, _i64, _i64, _p, _i, _p],
     "q27h_last_error": [],
@@ -83,7 +84,7 @@ SIGNATURES = {
 }
 _RESTYPE = {"q27h_kv_cache_bytes": _sz, "q27h_qmat_bytes": _sz, "q27h_last_error": C.c_char_p,
             "q27h_gtype_name": C.c_char_p, "q27h_gguf_close": None, "q27h_gguf_n_tensors": _i64, "q27h_gguf_find": _i64,
-            "q27h_gguf_n_kv": _i64, "q27h_gguf_key": C.c_char_p}
+            "q27h_gguf_n_kv": _i64}
 
 _lib = None
 

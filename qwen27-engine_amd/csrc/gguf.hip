@@ -129,10 +129,9 @@ struct q27h_gguf {
       } else if (t == kArr) {
         const uint32_t et = c.get<uint32_t>();
         const uint64_t n = c.get<uint64_t>();
-        if (n > (uint64_t)(c.end - c.p)) throw std::runtime_error("gguf: truncated file");  // >= 1 byte each
+        // elements are appended as read (nothing reserved from n): a corrupt count ends at the mapping's end
         if (et == kStr) {
           v.kind = Q27H_GV_ARR_STRING;
-          v.as.reserve(n);
           for (uint64_t j = 0; j < n; j++) v.as.push_back(c.str());
         } else {
           int64_t iv = 0;
@@ -317,36 +316,51 @@ extern "C" int q27h_gguf_tensor(const q27h_gguf* g, int64_t i, q27h_gtensor* out
 
 extern "C" int64_t q27h_gguf_n_kv(const q27h_gguf* g) { return g ? (int64_t)g->keys.size() : 0; }
 
-extern "C" const char* q27h_gguf_key(const q27h_gguf* g, int64_t i) {
-  if (!g || i < 0 || i >= (int64_t)g->keys.size()) return nullptr;
-  return g->keys[i].c_str();
+extern "C" int q27h_gguf_key(const q27h_gguf* g, int64_t i, const char** s, size_t* len) {
+  if (!g || !s || !len) return fail(Q27H_ERR_ARG, "gguf_key: null pointer");
+  if (i < 0 || i >= (int64_t)g->keys.size()) return fail(Q27H_ERR_NOT_FOUND, "gguf_key: index out of range");
+  *s = g->keys[i].c_str();
+  *len = g->keys[i].size();
+  return Q27H_OK;
 }
+
+namespace {
+int fill_value(const Value& v, q27h_gvalue* out) {
+  out->kind = v.kind;
+  out->i = v.i;
+  out->f = v.f;
+  out->s = v.s.c_str();
+  out->s_len = v.s.size();
+  out->n = v.kind == Q27H_GV_ARR_INT ? v.ai.size()
+           : v.kind == Q27H_GV_ARR_FLOAT ? v.af.size()
+           : v.kind == Q27H_GV_ARR_STRING ? v.as.size() : 0;
+  out->ai = v.ai.empty() ? nullptr : v.ai.data();
+  out->af = v.af.empty() ? nullptr : v.af.data();
+  return Q27H_OK;
+}
+}  // namespace
 
 extern "C" int q27h_gguf_kv(const q27h_gguf* g, const char* key, q27h_gvalue* out) {
   if (!g || !key || !out) return fail(Q27H_ERR_ARG, "gguf_kv: null pointer");
   const Value* v = find_kv(g, key);
   if (!v) return fail(Q27H_ERR_NOT_FOUND, std::string("missing key ") + key);
-  out->kind = v->kind;
-  out->i = v->i;
-  out->f = v->f;
-  out->s = v->s.c_str();
-  out->s_len = v->s.size();
-  out->n = v->kind == Q27H_GV_ARR_INT ? v->ai.size()
-           : v->kind == Q27H_GV_ARR_FLOAT ? v->af.size()
-           : v->kind == Q27H_GV_ARR_STRING ? v->as.size() : 0;
-  out->ai = v->ai.empty() ? nullptr : v->ai.data();
-  out->af = v->af.empty() ? nullptr : v->af.data();
-  return Q27H_OK;
+  return fill_value(*v, out);
 }
 
-extern "C" int q27h_gguf_kv_str_at(const q27h_gguf* g, const char* key, uint64_t j, const char** s, size_t* len) {
-  if (!g || !key || !s || !len) return fail(Q27H_ERR_ARG, "gguf_kv_str_at: null pointer");
-  const Value* v = find_kv(g, key);
-  if (!v) return fail(Q27H_ERR_NOT_FOUND, std::string("missing key ") + key);
-  if (v->kind != Q27H_GV_ARR_STRING) return fail(Q27H_ERR_FORMAT, std::string("key is not a string array: ") + key);
-  if (j >= v->as.size()) return fail(Q27H_ERR_NOT_FOUND, std::string("index out of range for ") + key);
-  *s = v->as[j].c_str();
-  *len = v->as[j].size();
+extern "C" int q27h_gguf_kv_at(const q27h_gguf* g, int64_t i, q27h_gvalue* out) {
+  if (!g || !out) return fail(Q27H_ERR_ARG, "gguf_kv_at: null pointer");
+  if (i < 0 || i >= (int64_t)g->keys.size()) return fail(Q27H_ERR_NOT_FOUND, "gguf_kv_at: index out of range");
+  return fill_value(g->kv.at(g->keys[i]), out);
+}
+
+extern "C" int q27h_gguf_kv_str_at(const q27h_gguf* g, int64_t i, uint64_t j, const char** s, size_t* len) {
+  if (!g || !s || !len) return fail(Q27H_ERR_ARG, "gguf_kv_str_at: null pointer");
+  if (i < 0 || i >= (int64_t)g->keys.size()) return fail(Q27H_ERR_NOT_FOUND, "gguf_kv_str_at: index out of range");
+  const Value& v = g->kv.at(g->keys[i]);
+  if (v.kind != Q27H_GV_ARR_STRING) return fail(Q27H_ERR_FORMAT, "key is not a string array: " + g->keys[i]);
+  if (j >= v.as.size()) return fail(Q27H_ERR_NOT_FOUND, "index out of range for " + g->keys[i]);
+  *s = v.as[j].c_str();
+  *len = v.as[j].size();
   return Q27H_OK;
 }
 

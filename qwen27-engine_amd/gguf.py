@@ -84,6 +84,7 @@ class GGUF:
         self._h = h
         self.path = str(path)
         self._tensors = None
+        self._keys = None
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -120,17 +121,28 @@ class GGUF:
             raise Q27Error(-7, f"missing tensor {name}")
         return t
 
+    def _key_index(self) -> dict:
+        if self._keys is None:
+            sp, n = C.c_void_p(), C.c_size_t()
+            keys = {}
+            for i in range(lib().q27h_gguf_n_kv(self._h)):
+                check(lib().q27h_gguf_key(self._h, i, C.byref(sp), C.byref(n)))
+                keys[C.string_at(sp.value, n.value).decode("utf-8", "surrogateescape")] = i
+            self._keys = keys
+        return self._keys
+
     def keys(self) -> list:
-        return [lib().q27h_gguf_key(self._h, i).decode("utf-8", "surrogateescape")
-                for i in range(lib().q27h_gguf_n_kv(self._h))]
+        return list(self._key_index())
 
     def has(self, key: str) -> bool:
-        v = GValueC()
-        return lib().q27h_gguf_kv(self._h, key.encode(), C.byref(v)) == 0
+        return key in self._key_index()
 
     def kv(self, key: str) -> GValue:
+        i = self._key_index().get(key)
+        if i is None:
+            raise Q27Error(-7, f"missing key {key}")
         v = GValueC()
-        check(lib().q27h_gguf_kv(self._h, key.encode(), C.byref(v)))
+        check(lib().q27h_gguf_kv_at(self._h, i, C.byref(v)))
         out = GValue(v.kind, v.i, v.f)
         if v.kind == STRING:
             out.s = C.string_at(v.s, v.s_len).decode("utf-8", "surrogateescape")
@@ -142,7 +154,7 @@ class GGUF:
             sp, n = C.c_void_p(), C.c_size_t()
             items = []
             for j in range(v.n):
-                check(lib().q27h_gguf_kv_str_at(self._h, key.encode(), j, C.byref(sp), C.byref(n)))
+                check(lib().q27h_gguf_kv_str_at(self._h, i, j, C.byref(sp), C.byref(n)))
                 items.append(C.string_at(sp.value, n.value).decode("utf-8", "surrogateescape"))
             out.as_ = tuple(items)
         return out
