@@ -101,6 +101,12 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise Q27Error(-3, f"{LIB_PATH} is missing: build it with build_library() (or __graft_entry__.build())")
+        # torch ships its own HIP runtime (same soname); loading it first makes the library bind to that one
+        # instead of pulling a second runtime from /opt/rocm into the process
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
