@@ -1,7 +1,8 @@
-"""The C++ drop-in headers at run time: tests/cpp/libdropin_layer.so calls q27::sum_norm_q8, gdn_conv_l2,
-gdn_step, gated_rmsnorm_q8, gdn_conv_prefill and gdn_flip_plane exactly as src/model.cu does for a GDN layer
-(decode with snapshots, and prefill in flip mode); every output is compared bit for bit with the oracle run through
-the same sequence. A bad shape must surface as the reference's std::runtime_error (checked on the CPU)."""
+"""The C++ drop-in headers at run time: tests/cpp/libdropin_layer.so calls the q27:: functions exactly as
+src/model.cu does -- a GDN layer (decode with snapshots, prefill in flip mode), the fused ops of an attention + FFN
+prefill layer, and a decode GEMV whose weights are read with q27::GGUF and uploaded with qmat_upload -- and every
+output is compared bit for bit with the oracle run through the same sequence. A bad shape must surface as the
+reference's std::runtime_error (checked on the CPU)."""
 import ctypes as C
 import os
 import sys
@@ -121,3 +122,84 @@ def test_gdn_prefill_layer_through_cpp_headers(q27, oracle, dl, dev, M, pin):
                             (oxs, gs, "o xs")):
         assert_bits_equal(down(got), want, what)
     assert int(plane.item()) == 1 - pin  # gdn_flip_plane
+
+
+@pytest.mark.gpu
+def test_attn_ffn_prefill_through_cpp_headers(q27, oracle, dl, dev):
+    import torch
+
+    M, FF, n_ctx, pos0 = 96, 17408, 4096, 1000
+    say(f"C++ drop-in attention + FFN prefill M={M}")
+    r = cd.rng(950)
+    kind = "iq2_s"
+    bb, bv = cd.BLOCK[kind]
+    row_bytes = E // bv * bb
+    table = cd.random_table(r, kind, 4096, E)
+    ids = r.integers(0, 4096, M).astype(np.int32)
+    w_attn, w_ffn = cd.normal(r, E, 0.1, 1.0), cd.normal(r, E, 0.1, 1.0)
+    qg, k, v = cd.normal(r, M * cd.NQH * 512), cd.normal(r, M * cd.NKVH * 256), cd.normal(r, M * cd.NKVH * 256)
+    qw, kw = cd.normal(r, 256, 0.1, 1.0), cd.normal(r, 256, 0.1, 1.0)
+    partial, gate, up, ao = cd.normal(r, M * E), cd.normal(r, M * FF, 2.0), cd.normal(r, M * FF, 2.0), cd.normal(r, M * 6144)
+    upd = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device=dev)  # noqa: E731
+    nb = q27.ops.kv_cache_bytes(cd.NKVH, n_ctx, True)
+    dt_, dids, x = upd(table), upd(ids), z(M * E)
+    h, xq, xd, xs = z(M * E), z(M * E, torch.int8), z(M * E // 32), z(M * E // 16)
+    qn, kc, vc = z(M * cd.NQH * 256), z(nb, torch.uint8), z(nb, torch.uint8)
+    xq2, xd2, xs2 = z(M * E, torch.int8), z(M * E // 32), z(M * E // 16)
+    gq, gd, gs = z(M * FF, torch.int8), z(M * FF // 32), z(M * FF // 16)
+    aq, ad = z(M * 6144, torch.int8), z(M * 6144 // 32)
+    ins = [upd(a) for a in (w_attn, qg, k, v, qw, kw, partial, w_ffn, gate, up, ao)]
+    dw_attn, dqg, dk, dv, dqw, dkw, dpartial, dw_ffn, dgate, dup, dao = ins
+    p = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+    err = C.create_string_buffer(512)
+    s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = dl.dropin_attn_prefill(M, p(dt_), C.c_int64(row_bytes), p(dids), p(x), p(dw_attn), p(h), p(xq), p(xd), p(xs),
+                                p(dqg), p(dk), p(dv), p(dqw), p(dkw), p(qn), p(kc), p(vc), p(upd(np.array([pos0], np.int32))),
+                                n_ctx, C.c_float(cd.THETA_SCALE), p(dpartial), p(dw_ffn), p(xq2), p(xd2), p(xs2), p(dgate),
+                                p(dup), FF, p(gq), p(gd), p(gs), p(dao), p(aq), p(ad), s, err, 512)
+    assert rc == 0, err.value
+    torch.cuda.synchronize()
+    ox = oracle.get_rows(kind, table, row_bytes, ids, E)
+    oh, oq, od, os_ = oracle.rmsnorm_q8(ox, w_attn, E, M, EPS, with_h=True, with_xs=True)
+    okc, ovc = np.zeros(nb, np.uint8), np.zeros(nb, np.uint8)
+    oqn = oracle.attn_prep(qg, k, v, qw, kw, okc, ovc, pos0, M, EPS, cd.THETA_SCALE, cd.NQH, cd.NKVH, n_ctx, True)
+    ox2, _, oq2, od2, os2 = oracle.sum_norm_rows(ox, partial, w_ffn, E, M, EPS)
+    ogq, ogd, ogs = oracle.swiglu_q8(gate, up, with_xs=True)
+    oaq, oad, _ = oracle.quantize_q8_1(ao, 6144, M)
+    down = lambda t: t.cpu().numpy()  # noqa: E731
+    for got, want, what in ((x, ox2, "x"), (h, oh, "h"), (xq, oq, "attn xq"), (xd, od, "attn xd"), (xs, os_, "attn xs"),
+                            (qn, oqn, "qn"), (kc, okc, "kcache"), (vc, ovc, "vcache"), (xq2, oq2, "ffn xq"),
+                            (xd2, od2, "ffn xd"), (xs2, os2, "ffn xs"), (gq, ogq, "swiglu xq"), (gd, ogd, "swiglu xd"),
+                            (gs, ogs, "swiglu xs"), (aq, oaq, "quantize xq"), (ad, oad, "quantize xd")):
+        assert_bits_equal(down(got), want, what)
+
+
+@pytest.mark.gpu
+def test_gguf_gemv_through_cpp_headers(q27, oracle, dl, dev, tmp_path):
+    import torch
+
+    import gguf_writer as W
+
+    say("C++ drop-in GGUF -> qmat_upload -> qgemv")
+    r = cd.rng(960)
+    N, K, nc = 1024, 5120, 4
+    raw = cd.random_weights(r, cd.Q6_K, N, K)
+    path = tmp_path / "m.gguf"
+    path.write_bytes(W.build([("general.architecture", W.STR, "qwen35")],
+                             [("blk.0.ffn_down.weight", cd.Q6_K, (K, N), raw.tobytes())]))
+    xq, xd = cd.q8_activations(oracle, r, nc, K)
+    scratch = torch.empty(raw.size, dtype=torch.uint8, device=dev)
+    y = torch.zeros(nc * N, device=dev)
+    err = C.create_string_buffer(512)
+    s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dxq, dxd = torch.from_numpy(xq).to(dev), torch.from_numpy(xd).to(dev)
+    rc = dl.dropin_gguf_gemv(str(path).encode(), b"blk.0.ffn_down.weight", C.c_void_p(dxq.data_ptr()),
+                             C.c_void_p(dxd.data_ptr()), C.c_void_p(y.data_ptr()), nc, C.c_void_p(scratch.data_ptr()),
+                             C.c_size_t(raw.size), s, err, 512)
+    assert rc == 0, err.value
+    torch.cuda.synchronize()
+    assert_bits_equal(y.cpu().numpy().reshape(nc, N), oracle.qgemv(cd.Q6_K, raw, N, K, xq, xd, nc), "gguf gemv")
+    rc = dl.dropin_gguf_gemv(str(path).encode(), b"blk.0.missing", C.c_void_p(dxq.data_ptr()), C.c_void_p(dxd.data_ptr()),
+                             C.c_void_p(y.data_ptr()), nc, C.c_void_p(scratch.data_ptr()), C.c_size_t(raw.size), s, err, 512)
+    assert rc == 1 and err.value == b"missing tensor blk.0.missing"
