@@ -597,7 +597,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--graph-replays", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
-    ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--calib-copy", action="store_true", help="also run a plain 256 MiB copy (rocprof counter calibration)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
@@ -757,11 +757,11 @@ def main():
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
-        gbs1, secs1 = cpu_baseline(args.cpu_rows // 4, 1)
+        gbs1, secs1 = cpu_baseline(args.cpu_rows // 8, 1)
         gbsn, secsn = cpu_baseline(args.cpu_rows, threads)
         cpu = {"value": round(gbsn, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": (f"the prefill pass (64 layers, 322 launches of the oracle) on {args.cpu_rows} token rows split over "
-                          f"{threads} threads: {secsn:.1f} s; single thread on {args.cpu_rows // 4} rows: {gbs1:.3f} GB/s "
+                          f"{threads} threads: {secsn:.1f} s; single thread on {args.cpu_rows // 8} rows: {gbs1:.3f} GB/s "
                           f"({secs1:.1f} s)"),
                "single_thread_GBps": round(gbs1, 3),
                "us_per_2048_batch_equiv": round(step_bytes / (gbsn * 1e9) * 1e6, 0)}
