@@ -112,3 +112,16 @@ def test_qgemv_replays_in_hip_graph(q27, oracle, dev):
         g.replay()
         torch.cuda.synchronize()
         assert_bits_equal(y.cpu().numpy(), want, "qgemv graph replay")
+
+
+@pytest.mark.parametrize("type_", [cd.Q6_K, cd.IQ3_S])
+def test_qgemv_lm_head_shape(q27, oracle, dev, type_):
+    """The output projection (src/model.cu:236): 248320 vocabulary rows x 5120, 31040 tiles in one launch."""
+    N, K = 248320, 5120
+    say(f"qgemv LM head type {type_} {N}x{K}")
+    r = cd.rng(700 + type_)
+    raw = cd.random_weights(r, type_, N, K)
+    xq, xd = cd.q8_activations(oracle, r, 1, K)
+    got = _run(q27, dev, type_, N, K, raw, xq, xd, 1)
+    want = oracle.qgemv(type_, raw, N, K, xq, xd, 1)
+    assert_bits_equal(got, want, f"qgemv LM head type {type_}")
