@@ -253,18 +253,23 @@ __device__ __forceinline__ float half_lo(uint32_t w) { return h2f_bits((uint16_t
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f_bits((uint16_t)(w >> 16)); }
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-#ifndef Q27H_QG_NT
-#define Q27H_QG_NT 1
+// Cache policy of the weight loads. The small per-chunk fields and scales: nontemporal (SMALL). The wide
+// interleaved pieces: chosen per launch from K (kNtPiecesMaxK): nontemporal for K <= 8192 (many tiles of short rows),
+// ordinary loads beyond. Measured (us, T = 1, nontemporal / ordinary pieces): 5120 x 17408 Q6_K 17.9 / 16.6, Q4_K
+// 14.4 / 13.8, IQ4_XS 15.9 / 15.0, Q2_K 11.1 / 10.6; 17408 x 5120 Q6_K 14.6 / 15.2, Q4_K 11.0 / 11.4, IQ4_XS 12.1 /
+// 12.7. rocprofv3 FETCH_SIZE shows why: with nontemporal pieces a 5120 x 17408 Q6_K launch fetches 96 MB for its
+// 73 MB matrix, with ordinary loads exactly 73 MB.
+constexpr int kNtPiecesMaxK = 8192;
+#ifndef Q27H_QG_NT_SMALL
+#define Q27H_QG_NT_SMALL 1
 #endif
-template <int N>
-__device__ __forceinline__ void ld16(uint32_t* w, const uint8_t* p) {  // N x 16 bytes, streaming (read once)
+template <int N, bool NT = Q27H_QG_NT_SMALL>
+__device__ __forceinline__ void ld16(uint32_t* w, const uint8_t* p) {  // N x 16 bytes, read once
 #pragma unroll
   for (int i = 0; i < N; i++) {
-#if Q27H_QG_NT
-    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p + i);
-#else
-    const u32x4 v = ((const u32x4*)p)[i];
-#endif
+    u32x4 v;
+    if constexpr (NT) v = __builtin_nontemporal_load((const u32x4*)p + i);
+    else v = ((const u32x4*)p)[i];
     w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
   }
 }
@@ -296,62 +301,62 @@ struct Chunk {
 };
 
 // N 16-byte pieces of a field wider than 16 bytes (pieces 512 bytes apart, see field_off)
-template <int N>
-__device__ __forceinline__ void ldp(uint32_t* w, const uint8_t* p) {
+template <int N, bool NTP>
+__device__ __forceinline__ void ldp_(uint32_t* w, const uint8_t* p) {
 #pragma unroll
-  for (int i = 0; i < N; i++) ld16<1>(w + 4 * i, p + 512 * i);
+  for (int i = 0; i < N; i++) ld16<1, NTP>(w + 4 * i, p + 512 * i);
 }
 
-template <int TYPE>
+template <int TYPE, bool NTP>
 __device__ __forceinline__ void load_chunk(Chunk<TYPE>& c, const Mat& m, size_t tile, int b, int s) {
   const size_t tb = tile * m.nb + b;
   if constexpr (TYPE == kQ4K) {
-    ldp<8>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
+    ldp_<8, NTP>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
     ld16<1>(c.w + 32, m.f[1] + field_off(16, tile, m.nb, b, s));
     ld16<2>(c.w + 36, m.d + tb * 32);
   } else if constexpr (TYPE == kQ6K) {
-    ldp<8>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
-    ldp<4>(c.w + 32, m.f[1] + field_off(64, tile, m.nb, b, s));
+    ldp_<8, NTP>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
+    ldp_<4, NTP>(c.w + 32, m.f[1] + field_off(64, tile, m.nb, b, s));
     ld16<1>(c.w + 48, m.f[2] + field_off(16, tile, m.nb, b, s));
     ld16<1>(c.w + 52, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ3S) {
-    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
-    ldp<2>(c.w + 16, m.f[1] + field_off(32, tile, m.nb, b, s));
+    ldp_<4, NTP>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ldp_<2, NTP>(c.w + 16, m.f[1] + field_off(32, tile, m.nb, b, s));
     const u32x2 h = *(const u32x2*)(m.f[2] + field_off(8, tile, m.nb, b, s));
     c.w[24] = h.x; c.w[25] = h.y;
     c.w[26] = *(const uint32_t*)(m.f[3] + field_off(4, tile, m.nb, b, s));
     ld16<1>(c.w + 27, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ4XS) {
-    ldp<8>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
+    ldp_<8, NTP>(c.w, m.f[0] + field_off(128, tile, m.nb, b, s));
     const u32x2 l = *(const u32x2*)(m.f[1] + field_off(8, tile, m.nb, b, s));
     c.w[32] = l.x; c.w[33] = l.y;
     ld16<1>(c.w + 34, m.d + tb * 16);
   } else if constexpr (TYPE == kQ2K) {
-    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ldp_<4, NTP>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
     ld16<1>(c.w + 16, m.f[1] + field_off(16, tile, m.nb, b, s));
     ld16<2>(c.w + 20, m.d + tb * 32);
   } else if constexpr (TYPE == kIQ2XXS) {
-    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ldp_<4, NTP>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
     ld16<1>(c.w + 16, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ2XS) {
-    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ldp_<4, NTP>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
     const u32x2 l = *(const u32x2*)(m.f[1] + field_off(8, tile, m.nb, b, s));
     c.w[16] = l.x; c.w[17] = l.y;
     ld16<1>(c.w + 18, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ3XXS) {
-    ldp<4>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
-    ldp<2>(c.w + 16, m.f[1] + field_off(32, tile, m.nb, b, s));
+    ldp_<4, NTP>(c.w, m.f[0] + field_off(64, tile, m.nb, b, s));
+    ldp_<2, NTP>(c.w + 16, m.f[1] + field_off(32, tile, m.nb, b, s));
     ld16<1>(c.w + 24, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ2S) {
-    ldp<2>(c.w, m.f[0] + field_off(32, tile, m.nb, b, s));
-    ldp<2>(c.w + 8, m.f[1] + field_off(32, tile, m.nb, b, s));
+    ldp_<2, NTP>(c.w, m.f[0] + field_off(32, tile, m.nb, b, s));
+    ldp_<2, NTP>(c.w + 8, m.f[1] + field_off(32, tile, m.nb, b, s));
     const u32x2 h = *(const u32x2*)(m.f[2] + field_off(8, tile, m.nb, b, s));
     c.w[16] = h.x; c.w[17] = h.y;
     const u32x2 l = *(const u32x2*)(m.f[3] + field_off(8, tile, m.nb, b, s));
     c.w[18] = l.x; c.w[19] = l.y;
     ld16<1>(c.w + 20, m.d + tb * 16);
   } else if constexpr (TYPE == kIQ1M) {
-    ldp<2>(c.w, m.f[0] + field_off(32, tile, m.nb, b, s));
+    ldp_<2, NTP>(c.w, m.f[0] + field_off(32, tile, m.nb, b, s));
     ld16<1>(c.w + 8, m.f[1] + field_off(16, tile, m.nb, b, s));
     const u32x2 l = *(const u32x2*)(m.f[2] + field_off(8, tile, m.nb, b, s));
     c.w[12] = l.x; c.w[13] = l.y;
@@ -670,7 +675,7 @@ constexpr int waves_per_tile(int K) {
   return w < 1 ? 1 : w > kMaxW ? kMaxW : w;
 }
 
-template <int TYPE, int NC>
+template <int TYPE, int NC, bool NTP>
 __global__ void __launch_bounds__(64 * kMaxW) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                     float* __restrict__ y, int K, int W) {
   constexpr int LW = LutInfo<TYPE>::words;
@@ -735,16 +740,16 @@ __global__ void __launch_bounds__(64 * kMaxW) qgemv_kernel(Mat m, const int8_t* 
         dy[c] = xd[(size_t)c * (K / 32) + bb * 8 + s];
       }
     };
-    if (b < m.nb) load_chunk<TYPE>(ca, m, (size_t)tile, b, s);
+    if (b < m.nb) load_chunk<TYPE, NTP>(ca, m, (size_t)tile, b, s);
     while (b < m.nb) {
       load_x(b);
       const int b1 = b + step;
-      load_chunk<TYPE>(cb, m, (size_t)tile, b1 < m.nb ? b1 : b, s);
+      load_chunk<TYPE, NTP>(cb, m, (size_t)tile, b1 < m.nb ? b1 : b, s);
       dot_chunk<TYPE, NC>(ca, u, dy, lut, kv, acc);
       if (b1 >= m.nb) break;
       load_x(b1);
       const int b2 = b1 + step;
-      load_chunk<TYPE>(ca, m, (size_t)tile, b2 < m.nb ? b2 : b1, s);
+      load_chunk<TYPE, NTP>(ca, m, (size_t)tile, b2 < m.nb ? b2 : b1, s);
       dot_chunk<TYPE, NC>(cb, u, dy, lut, kv, acc);
       b = b2;
     }
@@ -784,7 +789,10 @@ template <int TYPE, int NC>
 void launch_gemv(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, hipStream_t s) {
   const int W = waves_per_tile(K);
   const int grid = m.ntiles;
-  hipLaunchKernelGGL((qgemv_kernel<TYPE, NC>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
+  if (K <= kNtPiecesMaxK)
+    hipLaunchKernelGGL((qgemv_kernel<TYPE, NC, true>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
+  else
+    hipLaunchKernelGGL((qgemv_kernel<TYPE, NC, false>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
 }
 
 template <int TYPE>
