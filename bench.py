@@ -426,6 +426,27 @@ GEMV_TYPES = {"iq3_s": (21, 110, (0,)), "q4_k": (12, 144, (0, 2)), "q6_k": (14, 
 GEMV_SHAPES = [(1024, 5120), (5120, 6144), (6144, 5120), (10240, 5120), (12288, 5120), (17408, 5120), (5120, 17408)]
 
 
+def gemv_profile(type_, N, K, T):
+    """Eight qgemv launches of one shape over four uploaded copies of a random matrix (for counter runs)."""
+    import torch
+
+    q27 = load_package()
+    q27.lib()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    bb = {10: 84, 12: 144, 14: 210, 16: 66, 17: 74, 18: 98, 21: 110, 22: 82, 23: 136, 29: 56}[type_]
+    raw = torch.randint(0, 256, (N * (K // 256) * bb,), dtype=torch.uint8, device=dev, generator=g)
+    mats = [q27.ops.qmat_upload(raw, type_, N, K) for _ in range(4)]
+    xq = torch.randint(-127, 128, (T * K,), dtype=torch.int8, device=dev, generator=g)
+    xd = torch.rand(T * K // 32, device=dev, generator=g) * 0.01
+    y = torch.empty(T * N, device=dev)
+    for i in range(8):
+        q27.ops.qgemv(mats[i % 4], xq, xd, y, T)
+    torch.cuda.synchronize()
+    log(f"gemv profile: type {type_} {N}x{K} T={T}, 8 launches")
+
+
 def bench_gemv(q27, torch):
     """Decode GEMV (the consumer of the q8_1 activations, src/qgemv.cu): per weight type and model shape, us per
     launch and GB/s of (matrix bytes + activations + y) with T = 4 and T = 1 activation columns. Enough distinct
@@ -598,6 +619,9 @@ def main():
     ap.add_argument("--graph-replays", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-rows", type=int, default=1024)
+    ap.add_argument("--gemv-profile", default=None, metavar="TYPE,N,K,T",
+                    help="only run eight decode GEMV launches of this shape over four uploaded copies of a random "
+                         "matrix (the workload of the rocprofv3 counter runs of the GEMV), then exit")
     ap.add_argument("--calib-copy", action="store_true", help="also run a plain 256 MiB copy (rocprof counter calibration)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
@@ -606,6 +630,9 @@ def main():
         print("bench.py measures one GPU: the fused-op path has no multi-GPU form in this build "
               "(sharding by token rows needs no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.gemv_profile:
+        gemv_profile(*[int(v) for v in args.gemv_profile.split(",")])
+        return
 
     import torch
 
