@@ -257,8 +257,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // interleaved pieces: chosen per launch from K (kNtPiecesMaxK): nontemporal for K <= 8192 (many tiles of short rows),
 // ordinary loads beyond. Measured (us, T = 1, nontemporal / ordinary pieces): 5120 x 17408 Q6_K 17.9 / 16.6, Q4_K
 // 14.4 / 13.8, IQ4_XS 15.9 / 15.0, Q2_K 11.1 / 10.6; 17408 x 5120 Q6_K 14.6 / 15.2, Q4_K 11.0 / 11.4, IQ4_XS 12.1 /
-// 12.7. rocprofv3 FETCH_SIZE shows why: with nontemporal pieces a 5120 x 17408 Q6_K launch fetches 96 MB for its
-// 73 MB matrix, with ordinary loads exactly 73 MB.
+// 12.7. rocprofv3 FETCH_SIZE shows why: with nontemporal pieces a 5120 x 17408 Q6_K launch fetches 98 MB for its
+// 73 MB matrix, with ordinary loads 75-77 MB.
 constexpr int kNtPiecesMaxK = 8192;
 #ifndef Q27H_QG_NT_SMALL
 #define Q27H_QG_NT_SMALL 1
