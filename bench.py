@@ -40,7 +40,7 @@ def is_attn(il):
     return (il + 1) % 4 == 0  # src/model.h:27
 
 
-# ---------------------------------------------------------------- algorithmic bytes (SURVEY 8d definitions)
+# ---------------------------------------------------------------- algorithmic bytes per unit of each op (read + write, compulsory)
 def bytes_rmsnorm_q8(rows, h, xs):
     return rows * (20480 + (20480 if h else 0) + 5120 + 640 + (1280 if xs else 0)) + 20480
 
@@ -628,7 +628,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the fused-op path has no multi-GPU form in this build "
-              "(sharding by token rows needs no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(sharding by token rows needs no exchange). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.gemv_profile:
         gemv_profile(*[int(v) for v in args.gemv_profile.split(",")])
