@@ -570,6 +570,47 @@ def bench_upload(q27, torch, gib=1.0):
     return out
 
 
+def bench_wire(q27, torch, M=2048):
+    """The two-card wire formats at the prefill batch (src/prefill.cu:338-406) on one GPU: to_q8_wire with carried
+    error feedback, add_norm_rows_q8 (h = null, xs) and to_bf16 of [M][5120], both q8 widths. Three buffer sets
+    are cycled; GB/s of the algorithmic bytes per launch."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(31)
+    out = {}
+    sets = 3
+    for qb in (16, 32):
+        rb = E + 2 * E // qb
+        p = [torch.randn(M * E, device=dev, generator=g) for _ in range(sets)]
+        ef = [torch.zeros(M * E, device=dev) for _ in range(sets)]
+        wire = [torch.zeros(M * rb, dtype=torch.uint8, device=dev) for _ in range(sets)]
+        for i in range(sets):
+            q27.ops.to_q8_wire(p[i], ef[i], True, wire[i], E, M, qb=qb)
+        us = time_back_to_back(torch, lambda i: q27.ops.to_q8_wire(p[i % sets], ef[i % sets], False, wire[i % sets], E, M,
+                                                                   qb=qb), 30)
+        b = M * (E * 4 * 2 + rb + E * 4)  # partial + ef in, wire + ef out
+        out[f"to_q8_wire_qb{qb}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "MB": round(b / 1e6, 1)}
+        x = [torch.randn(M * E, device=dev, generator=g) for _ in range(sets)]
+        w = torch.randn(E, device=dev, generator=g) * 0.1 + 1
+        xq, xd, xs = torch.empty(M * E, dtype=torch.int8, device=dev), torch.empty(M * E // 32, device=dev), torch.empty(
+            M * E // 16, device=dev)
+        us = time_back_to_back(torch, lambda i: q27.ops.add_norm_rows_q8(x[i % sets], wire[i % sets], wire[(i + 1) % sets], E,
+                                                                         M, w, EPS, None, xq, xd, xs, qb=qb), 30)
+        b = M * (E * 4 * 2 + 2 * rb + E + E // 32 * 4 + E // 16 * 4) + E * 4
+        out[f"add_norm_rows_q8_qb{qb}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "MB": round(b / 1e6, 1)}
+        log(f"  wire qb={qb}: to_q8_wire {out[f'to_q8_wire_qb{qb}']['us']} us, add_norm_rows_q8 "
+            f"{out[f'add_norm_rows_q8_qb{qb}']['us']} us")
+        del p, ef, wire, x
+    xs_ = [torch.randn(M * E, device=dev, generator=g) for _ in range(sets)]
+    y = torch.empty(M * E, dtype=torch.int16, device=dev)
+    us = time_back_to_back(torch, lambda i: q27.ops.to_bf16(xs_[i % sets], y, M * E), 30)
+    b = M * E * 6
+    out["to_bf16"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "MB": round(b / 1e6, 1)}
+    log(f"  wire: to_bf16 {us:.2f} us")
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_cfg1(q27, torch):
     """RMSNorm -> q8_1 of one 5120 row (0.1% outliers x50) on the CPU oracle and on the GPU, with the
     bit-exact comparison of xq / xd / xs."""
@@ -772,6 +813,7 @@ def main():
     torch.cuda.empty_cache()
     gdn_rec = bench_gdn(q27, torch)
     upload = bench_upload(q27, torch)
+    wire = bench_wire(q27, torch)
 
     if args.calib_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -815,6 +857,7 @@ def main():
         "decode_gemv": gemv,
         "gdn_recurrence": gdn_rec,
         "gguf_upload": upload,
+        "wire_formats": wire,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

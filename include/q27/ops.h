@@ -9,6 +9,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <stdexcept>
 #include <string>
 
@@ -99,6 +100,22 @@ struct ArArgs {
   int ef_first = 1;
   unsigned long long* tprof = nullptr;
 };
+
+// src/ops.h:119-120, src/ops.cu:20-30: values per scale on the two-card q8 wire, from Q27_WIRE (read once): "q8" 32,
+// "q8b16" 16 (the default), "bf16" 0; anything else throws.
+inline int wire_qb() {
+  static const int qb = [] {
+    const char* e = std::getenv("Q27_WIRE");
+    if (!e) return 16;
+    const std::string v(e);
+    if (v == "q8") return 32;
+    if (v == "q8b16") return 16;
+    if (v == "bf16") return 0;
+    throw std::runtime_error("Q27_WIRE: bf16, q8 or q8b16");
+  }();
+  return qb;
+}
+inline bool wire_q8() { return wire_qb() != 0; }
 
 // src/ops.h:99-100
 inline void rmsnorm_q8(const float* x, const float* w, float* h, int8_t* xq, float* xd, int n, int rows, float eps,

@@ -31,6 +31,19 @@ inline void sum_norm_rows(float* x, const float* partial, int n, int M, const Pf
 }
 // src/prefill.h:41
 inline void flip_plane_to(int* dst, const int* src, hipStream_t s) { q27h_check(q27h_flip_plane_to(dst, src, s)); }
+// src/prefill.h:34-35
+inline void to_bf16(const float* x, __hip_bfloat16* y, size_t n, hipStream_t s) {
+  q27h_check(q27h_to_bf16(x, reinterpret_cast<uint16_t*>(y), n, s));
+}
+// src/prefill.h:36-38 (the scale width of the wire is wire_qb(), as in the reference)
+inline void to_q8_wire(const float* partial, float* ef, bool first, uint8_t* wire, int n, int M, hipStream_t s) {
+  q27h_check(q27h_to_q8_wire(partial, ef, first ? 1 : 0, wire, n, M, wire_qb(), s));
+}
+// src/prefill.h:39-41
+inline void add_norm_rows_q8(float* x, const uint8_t* own, const uint8_t* recv, int n, int M, const float* w, float eps,
+                             float* h, int8_t* xq, float* xd, float* xs, hipStream_t s) {
+  q27h_check(q27h_add_norm_rows_q8(x, own, recv, n, M, w, eps, h, xq, xd, xs, wire_qb(), s));
+}
 // src/prefill.h:46-47 (recv = the other card's bf16 partial, or nullptr)
 inline void add_norm_rows(float* x, const float* partial, const __hip_bfloat16* recv, int n, int M, const float* w, float eps,
                           float* h, int8_t* xq, float* xd, float* xs, hipStream_t s) {

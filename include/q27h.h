@@ -113,6 +113,18 @@ int q27h_gdn_conv_prefill(const float* x, const float* w, float* planes, const i
 int q27h_gdn_flip_plane(int* plane, q27h_stream_t s);
 /* flip_plane_to (src/prefill.h:41, src/prefill.cu:515): *dst = (*src == 0 ? 1 : 0), enqueued. */
 int q27h_flip_plane_to(int* dst, const int* src, q27h_stream_t s);
+/* The wire formats of the two-card partial sum (src/prefill.h:34-44, src/prefill.cu:338-370,503-513); the transfer
+ * between cards is not part of this library. A q8 wire row of n = 5120 values is n int8 values, then n / qb fp16
+ * scales (qb = 16 "q8b16", 32 "q8"; the reference picks it from Q27_WIRE, src/ops.cu:20-30), 16-byte aligned.
+ * to_bf16: y = bf16(x) (round to nearest even), n even.
+ * to_q8_wire: per qb-value block of y = partial (+ ef unless first; ef may be NULL): q = roundf(y / (amax / 127)),
+ *   scale fp16(amax / 127); ef <- y - scale * q (error feedback).
+ * add_norm_rows_q8: x += (dequant(own) + dequant(recv)), then RMSNorm * w -> h (may be NULL), q8_1 and xs (may be
+ *   NULL), as add_norm_rows. */
+int q27h_to_bf16(const float* x, uint16_t* y, size_t n, q27h_stream_t s);
+int q27h_to_q8_wire(const float* partial, float* ef, int first, uint8_t* wire, int n, int M, int qb, q27h_stream_t s);
+int q27h_add_norm_rows_q8(float* x, const uint8_t* own, const uint8_t* recv, int n, int M, const float* w, float eps,
+                          float* h, int8_t* xq, float* xd, float* xs, int qb, q27h_stream_t s);
 
 /* ---------------------------------------------------------------- attention input stage */
 /* kv_cache_bytes (src/ops.h:54, src/attn.cu:890-892): bytes of one layer's K (or V) cache:

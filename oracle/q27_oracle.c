@@ -335,6 +335,66 @@ void q27o_add_norm_rows(float* x, const float* partial, const uint16_t* recv_bf1
   }
 }
 
+/* ---------------------------------------------------------------- wire formats of the two-card sum
+ * to_bf16 (src/prefill.cu:338-345): y = bf16(x), round to nearest even. */
+void q27o_to_bf16(const float* x, uint16_t* y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = q27o_f2bf(x[i]);
+}
+
+/* to_q8_wire (src/prefill.cu:347-370): per row of n values, y = partial (+ ef unless first); per block of qb values
+ * amax, d = amax / 127, q = amax == 0 ? 0 : roundf(y / d), scale fp16(d); ef = y - fp16(d) * q (a product, then a
+ * difference: no contraction). Row layout: n int8 values, then n / qb fp16 scales. */
+void q27o_to_q8_wire(const float* partial, float* ef, int first, uint8_t* wire, int n, int M, int qb) {
+  const size_t rb = (size_t)n + 2 * (size_t)n / qb;
+  for (int r = 0; r < M; r++) {
+    int8_t* q8 = (int8_t*)(wire + r * rb);
+    uint8_t* sc = wire + r * rb + n;
+    for (int b = 0; b < n / qb; b++) {
+      float y[32];
+      float amax = 0.0f;
+      for (int l = 0; l < qb; l++) {
+        const size_t i = (size_t)r * n + (size_t)b * qb + l;
+        y[l] = ef && !first ? partial[i] + ef[i] : partial[i];
+        amax = fmaxf(amax, fabsf(y[l]));
+      }
+      const float d = amax / 127.0f;
+      const uint16_t dh = q27o_f2h(d);
+      sc[2 * b] = (uint8_t)(dh & 0xff);
+      sc[2 * b + 1] = (uint8_t)(dh >> 8);
+      for (int l = 0; l < qb; l++) {
+        const int q = amax == 0.0f ? 0 : (int)roundf(y[l] / d);
+        q8[b * qb + l] = (int8_t)q;
+        if (ef) {
+          const float p = q27o_h2f(dh) * (float)q;
+          ef[(size_t)r * n + (size_t)b * qb + l] = y[l] - p;
+        }
+      }
+    }
+  }
+}
+
+/* add_norm_rows_q8 (src/prefill.cu:372-406): x += (dequant(own) + dequant(recv)) with dequant = fp16 scale * int8
+ * (both products exact), then the row norm of add_norm_rows. */
+void q27o_add_norm_rows_q8(float* x, const uint8_t* own, const uint8_t* recv, int n, int M, const float* w, float eps,
+                           float* h, int8_t* xq, float* xd, float* xs, int qb) {
+  const size_t rb = (size_t)n + 2 * (size_t)n / qb;
+  for (int r = 0; r < M; r++) {
+    float* xr = x + (size_t)r * n;
+    const int8_t* oq = (const int8_t*)(own + r * rb);
+    const int8_t* rq = (const int8_t*)(recv + r * rb);
+    const uint8_t* os = own + r * rb + n;
+    const uint8_t* rs = recv + r * rb + n;
+    for (int i = 0; i < n; i++) {
+      const int b = i / qb;
+      const float od = q27o_h2f((uint16_t)(os[2 * b] | (os[2 * b + 1] << 8)));
+      const float rd = q27o_h2f((uint16_t)(rs[2 * b] | (rs[2 * b + 1] << 8)));
+      const float a = od * (float)oq[i], c = rd * (float)rq[i];
+      xr[i] = xr[i] + (a + c);
+    }
+    norm_q8_row(xr, w, eps, n, (size_t)r, h, xq, xd, xs);
+  }
+}
+
 /* swiglu_q8 (src/ops.cu:262-270): silu(g) * u -> q8_1 over n values (n % 32 == 0). */
 void q27o_swiglu_q8(const float* g, const float* u, int8_t* xq, float* xd, int n, float* xs) {
   float y[32];

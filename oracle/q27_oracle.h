@@ -50,6 +50,11 @@ void q27o_sum_norm_rows(float* x, const float* partial, int n, int M, const floa
                         float* xd, float* xs);
 void q27o_add_norm_rows(float* x, const float* partial, const uint16_t* recv_bf16, int n, int M, const float* w, float eps,
                         float* h, int8_t* xq, float* xd, float* xs);
+/* wire formats of the two-card sum (src/prefill.cu:338-406); qb = values per fp16 scale (16 or 32) */
+void q27o_to_bf16(const float* x, uint16_t* y, size_t n);
+void q27o_to_q8_wire(const float* partial, float* ef, int first, uint8_t* wire, int n, int M, int qb);
+void q27o_add_norm_rows_q8(float* x, const uint8_t* own, const uint8_t* recv, int n, int M, const float* w, float eps,
+                           float* h, int8_t* xq, float* xd, float* xs, int qb);
 void q27o_swiglu_q8(const float* g, const float* u, int8_t* xq, float* xd, int n, float* xs);
 void q27o_gated_rmsnorm(const float* o, const float* w, const float* z, float* y, int n, int heads, float eps);
 void q27o_gated_rmsnorm_q8(const float* o, const float* w, const float* z, int8_t* xq, float* xd, int heads, float eps,

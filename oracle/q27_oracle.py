@@ -58,6 +58,9 @@ _SIGS = {
     "q27o_qgemv_block_bytes": (_i, [_i]),
     "q27o_qgemv_waves": (_i, [_i, _i]),
     "q27o_qgemv": (_i, [_i, _p, _i, _i, _p, _p, _p, _i]),
+    "q27o_to_bf16": (None, [_p, _p, C.c_size_t]),
+    "q27o_to_q8_wire": (None, [_p, _p, _i, _p, _i, _i, _i]),
+    "q27o_add_norm_rows_q8": (None, [_p, _p, _p, _i, _i, _p, C.c_float, _p, _p, _p, _p, _i]),
     "q27o_gdn_step": (_i, [_p, _p, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, C.c_float, _i, _i]),
     "q27o_gdn_step_parts": (_i, [_i, _p, _p, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, C.c_float, _i, _i]),
 }
@@ -334,3 +337,37 @@ def gdn_step(q, k, v, stride, g, beta, planes, in_plane, H, HK, T, scale, snapsh
     if rc != 0:
         raise ValueError("q27o_gdn_step: bad shape")
     return o, planes
+
+
+def wire_row_bytes(n, qb):
+    return n + 2 * n // qb
+
+
+def to_bf16(x):
+    x = _f32(x)
+    y = np.zeros(x.size, np.uint16)
+    lib().q27o_to_bf16(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def to_q8_wire(partial, ef, first, n, M, qb):
+    """Returns (wire uint8 [M][n + 2n/qb], ef after the call or None)."""
+    partial = _f32(partial)
+    ef = None if ef is None else _f32(ef).copy()
+    wire = np.zeros(M * wire_row_bytes(n, qb), np.uint8)
+    lib().q27o_to_q8_wire(_ptr(partial), _ptr(ef), int(first), _ptr(wire), n, M, qb)
+    return wire, ef
+
+
+def add_norm_rows_q8(x, own, recv, w, n, M, eps, qb, with_h=False, with_xs=True):
+    x = _f32(x).copy()
+    w = _f32(w)
+    own = np.ascontiguousarray(own, dtype=np.uint8)
+    recv = np.ascontiguousarray(recv, dtype=np.uint8)
+    h = np.zeros(M * n, np.float32) if with_h else None
+    xq = np.zeros(M * n, np.int8)
+    xd = np.zeros(M * n // 32, np.float32)
+    xs = np.zeros(M * n // 16, np.float32) if with_xs else None
+    lib().q27o_add_norm_rows_q8(_ptr(x), _ptr(own), _ptr(recv), n, M, _ptr(w), eps, _ptr(h), _ptr(xq), _ptr(xd), _ptr(xs),
+                                qb)
+    return x, h, xq, xd, xs

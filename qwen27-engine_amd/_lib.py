@@ -54,6 +54,9 @@ SIGNATURES = {
     "q27h_gdn_conv_prefill": [_p, _p, _p, _p, _p, _i, _i, _i, _f, _p, _p, _p, _p, _p, _p, _i, _p],
     "q27h_gdn_flip_plane": [_p, _p],
     "q27h_flip_plane_to": [_p, _p, _p],
+    "q27h_to_bf16": [_p, _p, _sz, _p],
+    "q27h_to_q8_wire": [_p, _p, _i, _p, _i, _i, _i, _p],
+    "q27h_add_norm_rows_q8": [_p, _p, _p, _i, _i, _p, _f, _p, _p, _p, _p, _i, _p],
     "q27h_kv_cache_bytes": [_i, _i, _i],
     "q27h_attn_prep": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _f, _f, _i, _i, _i, _i, _p, _p, _sz, _p, _p],
     "q27h_get_rows_iq2_s": [_p, _i64, _p, _i, _p, _i, _p, _p],

@@ -16,7 +16,7 @@ namespace q27h {
 namespace {
 
 // ---------------------------------------------------------------- row engine
-enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2 };
+enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2, kAddQ8Wire = 3 };
 #ifndef Q27H_ROW_NT
 #define Q27H_ROW_NT 0
 #endif
@@ -46,11 +46,15 @@ __device__ __forceinline__ float4 ld4_row(const float* p) {
 #endif
 }
 
+// MODE kAddQ8Wire: x += dequant(own) + dequant(recv), two q8 wire rows (wown, wrecv: n int8 values, then n / qb fp16
+// scales per row; qb = 1 << qb_shift values per scale).
 template <int MODE>
 __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x, const float* __restrict__ partial,
                                                           const uint16_t* __restrict__ recv, const float* __restrict__ w,
                                                           float eps, float* __restrict__ h, int8_t* __restrict__ xq,
-                                                          float* __restrict__ xd, float* __restrict__ xs) {
+                                                          float* __restrict__ xd, float* __restrict__ xs,
+                                                          const uint8_t* __restrict__ wown, const uint8_t* __restrict__ wrecv,
+                                                          int qb_shift) {
   __shared__ float red[32];
   const int t = threadIdx.x;
   const size_t row = blockIdx.x;
@@ -65,7 +69,25 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   }
 #pragma unroll
   for (int k = 0; k < 5; k++) wv[k] = ld4(w + off + k * 1024);  // issued before the reduction: no extra round trip
-  if constexpr (MODE != kPlain) {
+  if constexpr (MODE == kAddQ8Wire) {
+    // x[i] + (d_own q_own + d_recv q_recv): both products are exact (fp16 x int8), the sum rounds once
+    const size_t rb = kRowN + ((size_t)2 * kRowN >> qb_shift);
+    const uint8_t* ow = wown + row * rb;
+    const uint8_t* rw = wrecv + row * rb;
+#pragma unroll
+    for (int k = 0; k < 5; k++) {
+      const int i = off + k * 1024;
+      const uint32_t oq = *(const uint32_t*)(ow + i), rq = *(const uint32_t*)(rw + i);
+      const float od = h2f_bits(*(const uint16_t*)(ow + kRowN + 2 * (i >> qb_shift)));
+      const float rd = h2f_bits(*(const uint16_t*)(rw + kRowN + 2 * (i >> qb_shift)));
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float a = od * (float)(int8_t)(oq >> (8 * c)), b = rd * (float)(int8_t)(rq >> (8 * c));
+        v[k][c] = v[k][c] + (a + b);
+      }
+      st4<kRowNT>(x + base + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
+    }
+  } else if constexpr (MODE != kPlain) {
 #pragma unroll
     for (int k = 0; k < 5; k++) {
       const float4 p = ld4_row(partial + base + k * 1024);
@@ -293,10 +315,11 @@ int check_row_args(const char* fn, int n, int rows, const float* x, const float*
 
 template <int MODE>
 int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* recv, const float* w, float eps, float* h,
-                int8_t* xq, float* xd, float* xs, int rows, q27h_stream_t s) {
+                int8_t* xq, float* xd, float* xs, int rows, q27h_stream_t s, const uint8_t* wown = nullptr,
+                const uint8_t* wrecv = nullptr, int qb_shift = 0) {
   if (rows == 0) return Q27H_OK;
   hipLaunchKernelGGL(row_norm_q8_kernel<MODE>, dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h, xq, xd,
-                     xs);
+                     xs, wown, wrecv, qb_shift);
   return check_launch(fn);
 }
 
@@ -355,6 +378,16 @@ extern "C" int q27h_add_norm_rows(float* x, const float* partial, const uint16_t
     return launch_rows<kAddBf16Recv>("add_norm_rows", x, partial, recv, w, eps, h, xq, xd, xs, M, s);
   }
   return launch_rows<kAddPartial>("add_norm_rows", x, partial, nullptr, w, eps, h, xq, xd, xs, M, s);
+}
+
+extern "C" int q27h_add_norm_rows_q8(float* x, const uint8_t* own, const uint8_t* recv, int n, int M, const float* w,
+                                     float eps, float* h, int8_t* xq, float* xd, float* xs, int qb, q27h_stream_t s) {
+  if (qb != 16 && qb != 32) return fail(Q27H_ERR_SHAPE, "add_norm_rows_q8: qb must be 16 or 32 (the q8 wires)");
+  if (int e = check_row_args("add_norm_rows_q8", n, M, x, w, h, xq, xd)) return e;
+  if (M > 0 && (!own || !recv)) return fail(Q27H_ERR_ARG, "add_norm_rows_q8: null wire");
+  if (!aligned16(own) || !aligned16(recv)) return fail(Q27H_ERR_ARG, "add_norm_rows_q8: wires need 16-byte alignment");
+  return launch_rows<kAddQ8Wire>("add_norm_rows_q8", x, nullptr, nullptr, w, eps, h, xq, xd, xs, M, s, own, recv,
+                                 qb == 16 ? 4 : 5);
 }
 
 extern "C" int q27h_quantize_q8_1(const float* x, int8_t* xq, float* xd, int K, int ncols, q27h_stream_t s, float* xs) {

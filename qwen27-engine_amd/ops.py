@@ -129,6 +129,36 @@ def flip_plane_to(dst, src, s=None):
     check(lib().q27h_flip_plane_to(_ptr(dst), _ptr(src), _stream(s)))
 
 
+def wire_qb():
+    """src/ops.cu:20-30: values per scale on the q8 wire from Q27_WIRE (q8: 32, q8b16: 16, bf16: 0; default 16)."""
+    import os
+
+    v = os.environ.get("Q27_WIRE")
+    if v is None:
+        return 16
+    table = {"q8": 32, "q8b16": 16, "bf16": 0}
+    if v not in table:
+        raise ValueError("Q27_WIRE: bf16, q8 or q8b16")
+    return table[v]
+
+
+def to_bf16(x, y, n, s=None):
+    """src/prefill.h:35: y (bf16 as uint16 / int16 / bfloat16 tensor) = bf16(x)."""
+    check(lib().q27h_to_bf16(_ptr(x), _ptr(y), n, _stream(s)))
+
+
+def to_q8_wire(partial, ef, first, wire, n, M, s=None, qb=None):
+    """src/prefill.h:38: q8 wire rows of partial (+ ef unless first), ef <- rounding error (may be None)."""
+    check(lib().q27h_to_q8_wire(_ptr(partial), _ptr(ef), int(first), _ptr(wire), n, M, wire_qb() if qb is None else qb,
+                                _stream(s)))
+
+
+def add_norm_rows_q8(x, own, recv, n, M, w, eps, h, xq, xd, xs, s=None, qb=None):
+    """src/prefill.h:40-41: x += dequant(own) + dequant(recv), then RMSNorm * w -> h, q8_1, xs."""
+    check(lib().q27h_add_norm_rows_q8(_ptr(x), _ptr(own), _ptr(recv), n, M, _ptr(w), eps, _ptr(h), _ptr(xq), _ptr(xd),
+                                      _ptr(xs), wire_qb() if qb is None else qb, _stream(s)))
+
+
 def sum_norm_rows(x, partial, n, M, ex, w, eps, h, xq, xd, xs, s=None):
     check(lib().q27h_sum_norm_rows(_ptr(x), _ptr(partial), n, M, _ptr(ex), _ptr(w), eps, _ptr(h), _ptr(xq), _ptr(xd),
                                    _ptr(xs), _stream(s)))

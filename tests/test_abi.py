@@ -62,6 +62,13 @@ FAKE = 1 << 20  # an aligned non-null address: the calls below must fail before 
      "bad shape"),
     (lambda o: o.gdn_step(FAKE, FAKE + 8, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 4, 0.088, True, 0), -4,
      "alignment"),
+    (lambda o: o.to_q8_wire(FAKE, None, True, FAKE, 4096, 4, 0, 16), -1, "n must be 5120"),
+    (lambda o: o.to_q8_wire(FAKE, None, True, FAKE, 5120, 4, 0, 24), -1, "qb must be 16 or 32"),
+    (lambda o: o.add_norm_rows_q8(FAKE, FAKE, FAKE, 5120, 4, FAKE, 1e-6, None, FAKE, FAKE, None, 0, 0), -1,
+     "qb must be 16 or 32"),
+    (lambda o: o.add_norm_rows_q8(FAKE, FAKE, FAKE + 8, 5120, 4, FAKE, 1e-6, None, FAKE, FAKE, None, 0, 16), -4,
+     "alignment"),
+    (lambda o: o.to_bf16(FAKE, FAKE, 5, 0), -1, "even"),
     (lambda o: o.get_rows_q4_k(FAKE, 2880, FAKE, 4, FAKE, 5000, 0), -1, "multiple of 256"),
     (lambda o: o.get_rows_q8_0(FAKE, 100, FAKE, 4, FAKE, 5120, 0), -1, "row_bytes"),
     (lambda o: o.rmsnorm_q8(FAKE + 4, FAKE, None, FAKE, FAKE, 5120, 4, 1e-6, 0), -4, "alignment"),
@@ -100,6 +107,12 @@ void step(float* x, const float* part, const float* w, float* h, int8_t* xq, flo
   q27::quantize_q8_1(x, xq, xd, 6144, 2048, s, xs);
   q27::get_rows_iq2_s(emb, 1640, ids, 4, x, 5120, s);
   q27::gdn_flip_plane(plane, s);
+  if (q27::wire_q8()) {
+    q27::to_q8_wire(part, h, false, (uint8_t*)xq, 5120, 2048, s);  // src/prefill.h:38
+    q27::add_norm_rows_q8(x, (const uint8_t*)xq, (const uint8_t*)xq, 5120, 2048, w, 1e-6f, nullptr, xq, xd, xs, s);
+  } else {
+    q27::to_bf16(part, (__hip_bfloat16*)h, 5120, s);
+  }
   q27::gdn_step(x, x + 2048, x + 4096, 10240, g, u, h, plane, h, 48, 16, 4, 0.0884f, true, s);         // decode
   q27::gdn_step(x, x + 2048, x + 4096, 10240, g, u, h, plane, h, 48, 16, 2048, 0.0884f, false, s, true);  // prefill
   (void)q27::kv_cache_bytes(4, 180224, true);
