@@ -52,6 +52,12 @@ inline void gdn_gates(const float* a, const float* b, const float* ssm_a, const 
                       int T, hipStream_t s) {
   q27h_check(q27h_gdn_gates(a, b, ssm_a, dt_bias, g, beta, H, T, s));
 }
+// src/ops.h:24-26
+inline void gemv_bf16_pair(const __hip_bfloat16* Wa, const __hip_bfloat16* Wb, const float* x, float* ya, float* yb, int N,
+                           int K, int T, hipStream_t s) {
+  q27h_check(q27h_gemv_bf16_pair(reinterpret_cast<const uint16_t*>(Wa), reinterpret_cast<const uint16_t*>(Wb), x, ya, yb, N,
+                                 K, T, s));
+}
 // src/ops.h:32-33
 inline void gdn_conv(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,
                      bool snapshots, hipStream_t s) {

@@ -83,6 +83,11 @@ int q27h_gated_rmsnorm(const float* o, const float* w, const float* z, float* y,
 /* l2norm_heads (src/ops.h:34, src/ops.cu:781-783): x <- rms_norm(x, eps/n) / sqrt(n) per head of n values;
  * `heads` heads at the start of each of T rows of `stride` values. In place. */
 int q27h_l2norm_heads(float* x, int n, int heads, int T, int stride, float eps, q27h_stream_t s);
+/* gemv_bf16_pair (src/ops.h:24-26, src/ops.cu:377-393, 768-771): ya[t] = Wa x[t], yb[t] = Wb x[t] for two bf16
+ * matrices of N rows and K columns (ssm_alpha / ssm_beta), f32 x [T][K], in the reference's summation order.
+ * K % 8 == 0; Wa, Wb, x 16-byte aligned. */
+int q27h_gemv_bf16_pair(const uint16_t* Wa, const uint16_t* Wb, const float* x, float* ya, float* yb, int N, int K, int T,
+                        q27h_stream_t s);
 /* gdn_gates (src/ops.h:29-30, src/ops.cu:773-776): beta = sigmoid(b), g = softplus(a + dt_bias) * ssm_a, [T][H]. */
 int q27h_gdn_gates(const float* a, const float* b, const float* ssm_a, const float* dt_bias, float* g, float* beta, int H,
                    int T, q27h_stream_t s);

@@ -335,6 +335,25 @@ void q27o_add_norm_rows(float* x, const float* partial, const uint16_t* recv_bf1
   }
 }
 
+/* gemv_bf16_pair (src/ops.cu:377-393): per output row of [Wa; Wb] and token, 256 threads; thread v adds
+ * (w[k] x[k] + w[k + 1] x[k + 1]) for k = 2v, 2v + 512, ... < K, then block_sum. */
+void q27o_gemv_bf16_pair(const uint16_t* Wa, const uint16_t* Wb, const float* x, float* ya, float* yb, int N, int K, int T) {
+  float part[256];
+  for (int t = 0; t < T; t++)
+    for (int row = 0; row < 2 * N; row++) {
+      const uint16_t* w = row < N ? Wa + (size_t)row * K : Wb + (size_t)(row - N) * K;
+      const float* xt = x + (size_t)t * K;
+      for (int v = 0; v < 256; v++) {
+        float acc = 0.0f;
+        for (int k = 2 * v; k < K; k += 512) acc = acc + (q27o_bf2f(w[k]) * xt[k] + q27o_bf2f(w[k + 1]) * xt[k + 1]);
+        part[v] = acc;
+      }
+      const float y = block_sum(part, 256);
+      if (row < N) ya[(size_t)t * N + row] = y;
+      else yb[(size_t)t * N + row - N] = y;
+    }
+}
+
 /* ---------------------------------------------------------------- wire formats of the two-card sum
  * to_bf16 (src/prefill.cu:338-345): y = bf16(x), round to nearest even. */
 void q27o_to_bf16(const float* x, uint16_t* y, size_t n) {

@@ -50,6 +50,8 @@ void q27o_sum_norm_rows(float* x, const float* partial, int n, int M, const floa
                         float* xd, float* xs);
 void q27o_add_norm_rows(float* x, const float* partial, const uint16_t* recv_bf16, int n, int M, const float* w, float eps,
                         float* h, int8_t* xq, float* xd, float* xs);
+/* gemv_bf16_pair (src/ops.cu:377-393) */
+void q27o_gemv_bf16_pair(const uint16_t* Wa, const uint16_t* Wb, const float* x, float* ya, float* yb, int N, int K, int T);
 /* wire formats of the two-card sum (src/prefill.cu:338-406); qb = values per fp16 scale (16 or 32) */
 void q27o_to_bf16(const float* x, uint16_t* y, size_t n);
 void q27o_to_q8_wire(const float* partial, float* ef, int first, uint8_t* wire, int n, int M, int qb);

@@ -59,6 +59,7 @@ _SIGS = {
     "q27o_qgemv_waves": (_i, [_i, _i]),
     "q27o_qgemv": (_i, [_i, _p, _i, _i, _p, _p, _p, _i]),
     "q27o_to_bf16": (None, [_p, _p, C.c_size_t]),
+    "q27o_gemv_bf16_pair": (None, [_p, _p, _p, _p, _p, _i, _i, _i]),
     "q27o_to_q8_wire": (None, [_p, _p, _i, _p, _i, _i, _i]),
     "q27o_add_norm_rows_q8": (None, [_p, _p, _p, _i, _i, _p, C.c_float, _p, _p, _p, _p, _i]),
     "q27o_gdn_step": (_i, [_p, _p, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, C.c_float, _i, _i]),
@@ -371,3 +372,14 @@ def add_norm_rows_q8(x, own, recv, w, n, M, eps, qb, with_h=False, with_xs=True)
     lib().q27o_add_norm_rows_q8(_ptr(x), _ptr(own), _ptr(recv), n, M, _ptr(w), eps, _ptr(h), _ptr(xq), _ptr(xd), _ptr(xs),
                                 qb)
     return x, h, xq, xd, xs
+
+
+def gemv_bf16_pair(Wa, Wb, x, N, K, T):
+    """Wa, Wb: bf16 bit patterns (uint16) [N][K]; returns (ya [T][N], yb [T][N])."""
+    Wa = np.ascontiguousarray(Wa, dtype=np.uint16)
+    Wb = np.ascontiguousarray(Wb, dtype=np.uint16)
+    x = _f32(x)
+    ya = np.zeros(T * N, np.float32)
+    yb = np.zeros(T * N, np.float32)
+    lib().q27o_gemv_bf16_pair(_ptr(Wa), _ptr(Wb), _ptr(x), _ptr(ya), _ptr(yb), N, K, T)
+    return ya.reshape(T, N), yb.reshape(T, N)

@@ -367,6 +367,59 @@ extern "C" int q27h_l2norm_heads(float* x, int n, int heads, int T, int stride, 
   return check_launch("l2norm_heads");
 }
 
+namespace q27h {
+namespace {
+// gemv_bf16_pair (src/ops.cu:377-393): y[t][row] of the two bf16 matrices [Wa; Wb] (N rows each, K columns) in the
+// reference's arithmetic: 256 virtual threads, thread v adds (w[k] x[k] + w[k + 1] x[k + 1]) for k = 2v + 512 j in
+// order, then block_sum (warp xor butterflies, 8 warp sums, second butterfly). One wave per (row, token): lane l holds
+// the virtual threads 32 (l / 8) + 4 quad_of_lane(l % 8) + c, c = 0..3, so its four pairs are 8 consecutive values
+// (one 16-byte load of weights per step) and the warp butterfly is lane xor 7, 2, 1 plus the lane's own pairs; the
+// 8 warp sums live in the 8 lane groups and meet through lane xor 32, 16, 8 (the second butterfly's xor 4, 2, 1;
+// its xor 16 and 8 only add the zero entries).
+__global__ void __launch_bounds__(256) gemv_bf16_pair_kernel(const uint16_t* __restrict__ Wa, const uint16_t* __restrict__ Wb,
+                                                             const float* __restrict__ x, float* __restrict__ ya,
+                                                             float* __restrict__ yb, int N, int K, int T) {
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave >= 2 * N * T) return;  // whole waves
+  const int row = wave % (2 * N), t = wave / (2 * N);
+  const int l = threadIdx.x & 63;
+  const uint16_t* w = row < N ? Wa + (size_t)row * K : Wb + (size_t)(row - N) * K;
+  const float* xt = x + (size_t)t * K;
+  const int k0 = 2 * (32 * (l >> 3) + 4 * quad_of_lane(l & 7));
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = k0; k < K; k += 512) {
+    const uint4 wv = *(const uint4*)(w + k);
+    const float4 xa = ld4(xt + k), xb = ld4(xt + k + 4);
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const float xx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float w0 = bf16_to_f((uint16_t)(ww[c] & 0xffff)), w1 = bf16_to_f((uint16_t)(ww[c] >> 16));
+      acc[c] = acc[c] + (w0 * xx[2 * c] + w1 * xx[2 * c + 1]);
+    }
+  }
+  float v = vwarp_sum4(acc);
+  v = (v + 0.0f) + 0.0f;  // the second butterfly's xor 16 and xor 8 steps (zero entries)
+  v += lane_xor32(v);
+  v += lane_xor<16>(v);
+  v += lane_xor<8>(v);
+  if (l == 0) (row < N ? ya[(size_t)t * N + row] : yb[(size_t)t * N + row - N]) = v;
+}
+}  // namespace
+}  // namespace q27h
+
+extern "C" int q27h_gemv_bf16_pair(const uint16_t* Wa, const uint16_t* Wb, const float* x, float* ya, float* yb, int N,
+                                   int K, int T, q27h_stream_t s) {
+  if (N <= 0 || K <= 0 || K % 8 || T < 0) return fail(Q27H_ERR_SHAPE, "gemv_bf16_pair: bad shape (K % 8 == 0)");
+  if (T == 0) return Q27H_OK;
+  if (!Wa || !Wb || !x || !ya || !yb) return fail(Q27H_ERR_ARG, "gemv_bf16_pair: null pointer");
+  if (!aligned16(Wa) || !aligned16(Wb) || !aligned16(x))
+    return fail(Q27H_ERR_ARG, "gemv_bf16_pair: Wa, Wb and x need 16-byte alignment");
+  const int waves = 2 * N * T;
+  hipLaunchKernelGGL(gemv_bf16_pair_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream_of(s), Wa, Wb, x, ya, yb, N, K, T);
+  return check_launch("gemv_bf16_pair");
+}
+
 extern "C" int q27h_gdn_gates(const float* a, const float* b, const float* ssm_a, const float* dt_bias, float* g, float* beta,
                               int H, int T, q27h_stream_t s) {
   if (H <= 0 || T < 0) return fail(Q27H_ERR_SHAPE, "gdn_gates: bad shape");

@@ -62,6 +62,11 @@ def gdn_gates(a, b, ssm_a, dt_bias, g, beta, H, T, s=None):
     check(lib().q27h_gdn_gates(_ptr(a), _ptr(b), _ptr(ssm_a), _ptr(dt_bias), _ptr(g), _ptr(beta), H, T, _stream(s)))
 
 
+def gemv_bf16_pair(Wa, Wb, x, ya, yb, N, K, T, s=None):
+    """src/ops.h:24-26: ya[t] = Wa x[t], yb[t] = Wb x[t] (Wa, Wb bf16 [N][K] as 16-bit tensors)."""
+    check(lib().q27h_gemv_bf16_pair(_ptr(Wa), _ptr(Wb), _ptr(x), _ptr(ya), _ptr(yb), N, K, T, _stream(s)))
+
+
 def gdn_conv(x, w, planes, in_plane, y, C, T, snapshots, s=None):
     check(lib().q27h_gdn_conv(_ptr(x), _ptr(w), _ptr(planes), _ptr(in_plane), _ptr(y), C, T, int(snapshots), _stream(s)))
 

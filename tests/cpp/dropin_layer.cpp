@@ -22,17 +22,20 @@ int report(const std::exception& e, char* err, int errlen) {
 }
 }  // namespace
 
-// Decode, T <= 4 tokens: x += partial, norm -> h and q8_1; conv + l2 + gates with snapshots; the delta rule with
-// snapshots; gated norm -> q8_1 of o.
+// Decode, T <= 4 tokens: x += partial, norm -> h and q8_1; the bf16 alpha / beta projections of h; conv + l2 + gates
+// with snapshots; the delta rule with snapshots; gated norm -> q8_1 of o.
 extern "C" int dropin_gdn_decode(int T, float* x, const float* partial, const float* w_norm, float* h, int8_t* xq,
-                                 float* xd, const float* conv_in, const float* conv_w, float* conv_planes,
-                                 const int* plane, float* conv_y, const float* a, const float* b, const float* ssm_a,
+                                 float* xd, const __hip_bfloat16* w_alpha, const __hip_bfloat16* w_beta, float* ab,
+                                 const float* conv_in, const float* conv_w, float* conv_planes,
+                                 const int* plane, float* conv_y, const float* ssm_a,
                                  const float* dt_bias, float* g, float* beta, float* ssm_planes, float* o,
                                  const float* gnorm_w, const float* z, int8_t* oxq, float* oxd, hipStream_t s, char* err,
                                  int errlen) {
   try {
     q27::sum_norm_q8(x, partial, E, T, nullptr, w_norm, EPS, h, xq, xd, s);
-    q27::gdn_conv_l2(conv_in, conv_w, conv_planes, plane, conv_y, C, T, true, 2 * KH, EPS, a, b, ssm_a, dt_bias, g, beta, H, s);
+    q27::gemv_bf16_pair(w_alpha, w_beta, h, ab, ab + T * H, H, E, T, s);  // src/model.cu:776
+    q27::gdn_conv_l2(conv_in, conv_w, conv_planes, plane, conv_y, C, T, true, 2 * KH, EPS, ab, ab + T * H, ssm_a, dt_bias, g,
+                     beta, H, s);
     q27::gdn_step(conv_y, conv_y + KH * D, conv_y + 2 * KH * D, C, g, beta, ssm_planes, plane, o, H, KH, T,
                   1.0f / std::sqrt((float)D), true, s);
     q27::gated_rmsnorm_q8(o, gnorm_w, z, oxq, oxd, H * T, EPS, s);

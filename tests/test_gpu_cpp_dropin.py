@@ -66,22 +66,29 @@ def test_gdn_decode_layer_through_cpp_headers(q27, oracle, dl, dev, T, pin):
     y, g, beta = torch.zeros(T * CC, device=dev), torch.zeros(T * H, device=dev), torch.zeros(T * H, device=dev)
     o = torch.zeros(T * H * D, device=dev)
     oxq, oxd = torch.zeros(T * H * D, dtype=torch.int8, device=dev), torch.zeros(T * H * D // 32, device=dev)
+    bits = lambda a: (cd.to_bf16_values(a).view(np.uint32) >> 16).astype(np.uint16)  # noqa: E731
+    w_alpha, w_beta = bits(cd.normal(r, H * E, 0.02)), bits(cd.normal(r, H * E, 0.02))
+    ab = torch.zeros(2 * T * H, device=dev)
+    dwa, dwb = up(w_alpha.view(np.int16)), up(w_beta.view(np.int16))  # kept alive: the call takes raw pointers
     err = C.create_string_buffer(512)
     p = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
     s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    rc = dl.dropin_gdn_decode(T, p(d["x"]), p(d["partial"]), p(d["w_norm"]), p(h), p(xq), p(xd), p(d["conv_in"]),
-                              p(d["conv_w"]), p(d["conv_planes"]), p(plane), p(y), p(d["a"]), p(d["b"]), p(d["ssm_a"]),
+    rc = dl.dropin_gdn_decode(T, p(d["x"]), p(d["partial"]), p(d["w_norm"]), p(h), p(xq), p(xd),
+                              p(dwa), p(dwb), p(ab), p(d["conv_in"]),
+                              p(d["conv_w"]), p(d["conv_planes"]), p(plane), p(y), p(d["ssm_a"]),
                               p(d["dt_bias"]), p(g), p(beta), p(d["ssm_planes"]), p(o), p(d["gnorm_w"]), p(d["z"]),
                               p(oxq), p(oxd), s, err, 512)
     assert rc == 0, err.value
     torch.cuda.synchronize()
     ox, oh, oq, od = oracle.sum_norm_q8(i["x"], i["partial"], i["w_norm"], E, T, EPS)
+    oa, ob_ = oracle.gemv_bf16_pair(w_alpha, w_beta, oh, H, E, T)
     oy, ocp, og, ob = oracle.gdn_conv_l2(i["conv_in"], i["conv_w"], i["conv_planes"], pin, CC, T, True, 2 * KH, EPS,
-                                         i["a"], i["b"], i["ssm_a"], i["dt_bias"], H)
+                                         oa.reshape(-1), ob_.reshape(-1), i["ssm_a"], i["dt_bias"], H)
     oo, osp = oracle.gdn_step(oy, oy[KH * D:], oy[2 * KH * D:], CC, og, ob, i["ssm_planes"], pin, H, KH, T,
                               np.float32(1.0) / np.sqrt(np.float32(D)), True, False)
     gq, gd, _ = oracle.gated_rmsnorm_q8(oo, i["gnorm_w"], i["z"], H * T, EPS)
     down = lambda t: t.cpu().numpy()  # noqa: E731
+    assert_bits_equal(down(ab), np.concatenate([oa.reshape(-1), ob_.reshape(-1)]), "alpha / beta")
     for got, want, what in ((d["x"], ox, "x"), (h, oh, "h"), (xq, oq, "xq"), (xd, od, "xd"), (y, oy, "conv y"),
                             (d["conv_planes"], ocp, "conv planes"), (g, og, "g"), (beta, ob, "beta"), (o, oo, "o"),
                             (d["ssm_planes"], osp, "state planes"), (oxq, gq, "o xq"), (oxd, gd, "o xd")):
@@ -151,11 +158,12 @@ def test_attn_ffn_prefill_through_cpp_headers(q27, oracle, dl, dev):
     aq, ad = z(M * 6144, torch.int8), z(M * 6144 // 32)
     ins = [upd(a) for a in (w_attn, qg, k, v, qw, kw, partial, w_ffn, gate, up, ao)]
     dw_attn, dqg, dk, dv, dqw, dkw, dpartial, dw_ffn, dgate, dup, dao = ins
+    dpos0 = upd(np.array([pos0], np.int32))  # kept alive: the call takes raw pointers
     p = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
     err = C.create_string_buffer(512)
     s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     rc = dl.dropin_attn_prefill(M, p(dt_), C.c_int64(row_bytes), p(dids), p(x), p(dw_attn), p(h), p(xq), p(xd), p(xs),
-                                p(dqg), p(dk), p(dv), p(dqw), p(dkw), p(qn), p(kc), p(vc), p(upd(np.array([pos0], np.int32))),
+                                p(dqg), p(dk), p(dv), p(dqw), p(dkw), p(qn), p(kc), p(vc), p(dpos0),
                                 n_ctx, C.c_float(cd.THETA_SCALE), p(dpartial), p(dw_ffn), p(xq2), p(xd2), p(xs2), p(dgate),
                                 p(dup), FF, p(gq), p(gd), p(gs), p(dao), p(aq), p(ad), s, err, 512)
     assert rc == 0, err.value

@@ -91,3 +91,21 @@ def test_to_bf16(q27, oracle, dev, n, offset):
     got = y.cpu().numpy().view(np.uint16)
     assert_bits_equal(got[:n], oracle.to_bf16(x[offset:]), "bf16")
     assert got[n] == 0 and got[n + 1] == 0
+
+
+@pytest.mark.parametrize("N,K,T", [(48, 5120, 4), (48, 5120, 1), (5, 1032, 3)])
+def test_gemv_bf16_pair(q27, oracle, dev, N, K, T):
+    """ssm_alpha / ssm_beta of the decode GDN layer (src/model.cu:776), and a K that is not a multiple of 512."""
+    import torch
+
+    say(f"gemv_bf16_pair N={N} K={K} T={T}")
+    r = cd.rng(1300 + K + T)
+    bits = lambda a: cd.to_bf16_values(a).view(np.uint32).__rshift__(16).astype(np.uint16)  # noqa: E731
+    Wa, Wb = bits(cd.normal(r, N * K, 0.05)), bits(cd.normal(r, N * K, 0.05))
+    x = cd.normal(r, T * K)
+    ya, yb = torch.full((T * N,), float("nan"), device=dev), torch.full((T * N,), float("nan"), device=dev)
+    q27.ops.gemv_bf16_pair(up(dev, Wa.view(np.int16)), up(dev, Wb.view(np.int16)), up(dev, x), ya, yb, N, K, T)
+    torch.cuda.synchronize()
+    oa, ob = oracle.gemv_bf16_pair(Wa, Wb, x, N, K, T)
+    assert_bits_equal(ya.cpu().numpy(), oa.reshape(-1), "ya")
+    assert_bits_equal(yb.cpu().numpy(), ob.reshape(-1), "yb")

@@ -1,10 +1,12 @@
-"""Pins of the oracle's wire formats of the two-card sum (to_bf16, to_q8_wire, add_norm_rows_q8; CPU only).
+"""Pins of the oracle's wire formats of the two-card sum (to_bf16, to_q8_wire, add_norm_rows_q8) and of
+gemv_bf16_pair (CPU only).
 
 The reference ships no vectors for them (src/prefill.cu:338-406). Pins: bf16 rounding against an integer
 restatement of round-to-nearest-even (and the specials); closed-form q8 blocks (zero, one-hot, exact ties);
 the quantization error bound; the error-feedback identity (with ef carried, the sum of K dequantized rows stays
 within one rounding step of K times the partial, while without it the error grows with K); and add_norm_rows_q8 ==
-sum_norm_rows on the dequantized sum (the already pinned row engine).
+sum_norm_rows on the dequantized sum (the already pinned row engine). gemv_bf16_pair: one-hot rows, exact integer
+dots and a float64 bound.
 """
 import numpy as np
 import pytest
@@ -114,3 +116,42 @@ def test_add_norm_rows_q8_equals_unfused(oracle, qb):
     for g, wnt in zip(got, want):
         assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
                               wnt.view(np.uint32) if wnt.dtype == np.float32 else wnt)
+
+
+# ---------------------------------------------------------------- gemv_bf16_pair (src/ops.cu:377-393)
+def bf16_bits(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_gemv_bf16_pair_one_hot_and_integer_exact(oracle):
+    """One-hot rows pick single activations exactly; small-integer weights and activations make every partial sum
+    an exact integer, so the result must equal the exact dot product (a wrong index or a dropped pair fails)."""
+    N, K, T = 6, 5120, 3
+    r = np.random.default_rng(8)
+    x = r.standard_normal(T * K).astype(np.float32)
+    Wa = np.zeros((N, K), np.float32)
+    cols = r.integers(0, K, N)
+    Wa[np.arange(N), cols] = 1.0
+    Wb = r.integers(-3, 4, (N, K)).astype(np.float32)
+    xi = r.integers(-4, 5, T * K).astype(np.float32)
+    ya, _ = oracle.gemv_bf16_pair(bf16_bits(Wa), bf16_bits(Wb), x, N, K, T)
+    assert np.array_equal(ya, x.reshape(T, K)[:, cols])
+    _, yb = oracle.gemv_bf16_pair(bf16_bits(Wa), bf16_bits(Wb), xi, N, K, T)
+    assert np.array_equal(yb, xi.reshape(T, K) @ Wb.T)
+
+
+def test_gemv_bf16_pair_float64_bound(oracle):
+    N, K, T = 48, 5120, 4
+    r = np.random.default_rng(9)
+    Wa, Wb = (r.standard_normal((N, K)) * 0.05).astype(np.float32), (r.standard_normal((N, K)) * 0.05).astype(np.float32)
+    ba, bb = bf16_bits(Wa), bf16_bits(Wb)
+    x = r.standard_normal(T * K).astype(np.float32)
+    ya, yb = oracle.gemv_bf16_pair(ba, bb, x, N, K, T)
+    fa = (ba.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    fb = (bb.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    x64 = x.reshape(T, K).astype(np.float64)
+    for got, f in ((ya, fa), (yb, fb)):
+        want = x64 @ f.T
+        mag = np.abs(x64) @ np.abs(f).T
+        assert np.all(np.abs(got - want) <= 1e-6 * mag + 1e-30)
