@@ -16,7 +16,10 @@ __constant__ uint64_t c_iq2s_grid[1024] = {
 };
 
 enum Fmt { kIQ2S = 0, kQ4K = 1, kQ6K = 2, kQ80 = 3 };
-constexpr int kChunk = 5120;  // values per workgroup: one embedding row of the 27B model
+#ifndef Q27H_ROWS_CHUNK
+#define Q27H_ROWS_CHUNK 2560  // half a 5120 row: 9.8 / 10.1 / 10.3 / 9.9 us (Q8_0 / IQ2_S / Q6_K / Q4_K) vs 11.5 / 10.7 / 10.6 / 9.9 for whole rows and 10.7 / 11.3 / 10.5 / 10.3 for 1024
+#endif
+constexpr int kChunk = Q27H_ROWS_CHUNK;  // values per workgroup
 
 template <int F>
 struct FmtInfo;
