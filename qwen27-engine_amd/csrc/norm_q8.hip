@@ -36,7 +36,8 @@ enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2, kAddQ8Wire = 3 };
 #ifndef Q27H_GATED_G
 #define Q27H_GATED_G 2  // 25.2 us in the pass vs 25.5 with 1 and 27.7 with 4
 #endif
-constexpr int kGatedG = Q27H_GATED_G;  // groups of 8 heads per workgroup in gated_rmsnorm_q8
+constexpr int kGatedG = Q27H_GATED_G;
+constexpr int kLatencyRows = 64;  // row launches up to this many rows take the latency-bound kernel variants  // groups of 8 heads per workgroup in gated_rmsnorm_q8
 constexpr bool kRowNT = Q27H_NT_ROW, kSwigluNT = Q27H_NT_SWIGLU, kQuantNT = Q27H_NT_QUANT, kGatedNT = Q27H_NT_GATED;
 __device__ __forceinline__ float4 ld4_row(const float* p) {
 #if Q27H_ROW_NT
@@ -48,7 +49,7 @@ __device__ __forceinline__ float4 ld4_row(const float* p) {
 
 // MODE kAddQ8Wire: x += dequant(own) + dequant(recv), two q8 wire rows (wown, wrecv: n int8 values, then n / qb fp16
 // scales per row; qb = 1 << qb_shift values per scale).
-template <int MODE>
+template <int MODE, bool EXACT>
 __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x, const float* __restrict__ partial,
                                                           const uint16_t* __restrict__ recv, const float* __restrict__ w,
                                                           float eps, float* __restrict__ h, int8_t* __restrict__ xq,
@@ -56,33 +57,57 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
                                                           const uint8_t* __restrict__ wown, const uint8_t* __restrict__ wrecv,
                                                           int qb_shift) {
   __shared__ float red[32];
+  args_now(x, partial, recv, w, eps, h, xq, xd, xs, wown, wrecv, qb_shift);
   const int t = threadIdx.x;
   const size_t row = blockIdx.x;
   const int off = 32 * (t >> 3) + block_offset(t);  // this thread's 4 values in each 1024-value slice
   const size_t base = row * kRowN + off;
+  // every load of the row first (x, the added operands, w), one memory round trip
   float v[5][4];
   float4 wv[5];
+  constexpr int NP = MODE == kAddPartial || MODE == kAddBf16Recv ? 5 : 1;
+  constexpr int NR = MODE == kAddBf16Recv ? 5 : 1, NQ = MODE == kAddQ8Wire ? 5 : 1;
+  float4 pv4[NP];
+  uint2 rv2[NR];
+  uint32_t oq[NQ], rq[NQ];
+  uint16_t odb[NQ], rdb[NQ];
 #pragma unroll
   for (int k = 0; k < 5; k++) {
     const float4 a = ld4_row(x + base + k * 1024);
     v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
   }
+  if constexpr (MODE == kAddPartial || MODE == kAddBf16Recv) {
 #pragma unroll
-  for (int k = 0; k < 5; k++) wv[k] = ld4(w + off + k * 1024);  // issued before the reduction: no extra round trip
+    for (int k = 0; k < 5; k++) pv4[k] = ld4_row(partial + base + k * 1024);
+  }
+  if constexpr (MODE == kAddBf16Recv) {
+#pragma unroll
+    for (int k = 0; k < 5; k++) rv2[k] = *(const uint2*)(recv + base + k * 1024);
+  }
   if constexpr (MODE == kAddQ8Wire) {
-    // x[i] + (d_own q_own + d_recv q_recv): both products are exact (fp16 x int8), the sum rounds once
     const size_t rb = kRowN + ((size_t)2 * kRowN >> qb_shift);
     const uint8_t* ow = wown + row * rb;
     const uint8_t* rw = wrecv + row * rb;
 #pragma unroll
     for (int k = 0; k < 5; k++) {
       const int i = off + k * 1024;
-      const uint32_t oq = *(const uint32_t*)(ow + i), rq = *(const uint32_t*)(rw + i);
-      const float od = h2f_bits(*(const uint16_t*)(ow + kRowN + 2 * (i >> qb_shift)));
-      const float rd = h2f_bits(*(const uint16_t*)(rw + kRowN + 2 * (i >> qb_shift)));
+      oq[k] = *(const uint32_t*)(ow + i);
+      rq[k] = *(const uint32_t*)(rw + i);
+      odb[k] = *(const uint16_t*)(ow + kRowN + 2 * (i >> qb_shift));
+      rdb[k] = *(const uint16_t*)(rw + kRowN + 2 * (i >> qb_shift));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 5; k++) wv[k] = ld4(w + off + k * 1024);
+  loads_issued();
+  if constexpr (MODE == kAddQ8Wire) {
+    // x[i] + (d_own q_own + d_recv q_recv): both products are exact (fp16 x int8), the sum rounds once
+#pragma unroll
+    for (int k = 0; k < 5; k++) {
+      const float od = h2f_bits(odb[k]), rd = h2f_bits(rdb[k]);
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        const float a = od * (float)(int8_t)(oq >> (8 * c)), b = rd * (float)(int8_t)(rq >> (8 * c));
+        const float a = od * (float)(int8_t)(oq[k] >> (8 * c)), b = rd * (float)(int8_t)(rq[k] >> (8 * c));
         v[k][c] = v[k][c] + (a + b);
       }
       st4<kRowNT>(x + base + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
@@ -90,13 +115,12 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   } else if constexpr (MODE != kPlain) {
 #pragma unroll
     for (int k = 0; k < 5; k++) {
-      const float4 p = ld4_row(partial + base + k * 1024);
-      const float pv[4] = {p.x, p.y, p.z, p.w};
+      const float pv[4] = {pv4[k].x, pv4[k].y, pv4[k].z, pv4[k].w};
       if constexpr (MODE == kAddPartial) {
 #pragma unroll
         for (int c = 0; c < 4; c++) v[k][c] = v[k][c] + pv[c];
       } else {
-        const uint2 rb = *(const uint2*)(recv + base + k * 1024);
+        const uint2 rb = rv2[k];
         const float rv[4] = {bf16_to_f((uint16_t)(rb.x & 0xffff)), bf16_to_f((uint16_t)(rb.x >> 16)),
                              bf16_to_f((uint16_t)(rb.y & 0xffff)), bf16_to_f((uint16_t)(rb.y >> 16))};
 #pragma unroll
@@ -119,15 +143,18 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   __syncthreads();
   const float tot = red32_sum(red);
   const float scale = 1.0f / __builtin_sqrtf(tot / (float)kRowN + eps);
+  float y[5][4];
 #pragma unroll
   for (int k = 0; k < 5; k++) {
     const float ww[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
-    float y[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) y[c] = scale * v[k][c] * ww[c];
-    if (h) st4<kRowNT>(h + base + k * 1024, y[0], y[1], y[2], y[3]);
-    q8_1_store4<kRowNT>(y, xq, xd, xs, base + k * 1024);
+    for (int c = 0; c < 4; c++) y[k][c] = scale * v[k][c] * ww[c];
   }
+  if (h) {
+#pragma unroll
+    for (int k = 0; k < 5; k++) st4<kRowNT>(h + base + k * 1024, y[k][0], y[k][1], y[k][2], y[k][3]);
+  }
+  q8_1_store_n<kRowNT, 5, EXACT>(y, xq, xd, xs, base, 1024);
 }
 
 // ---------------------------------------------------------------- flat q8_1 producers
@@ -142,50 +169,49 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 #endif
 constexpr int kSwigluU = Q27H_FLAT_U, kQuantU = Q27H_QUANT_U;
 
-template <bool SWIGLU, int kFlatU, bool NT>
+template <bool SWIGLU, int kFlatU, bool NT, bool EXACT>
 __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                       int8_t* __restrict__ xq, float* __restrict__ xd,
                                                       float* __restrict__ xs, size_t n) {
   const size_t base = (size_t)blockIdx.x * (kFlatU * 1024) + 32 * (threadIdx.x >> 3) + block_offset(threadIdx.x);
   float4 a[kFlatU], b[kFlatU];
+  int kn = 0;  // chunks of this lane inside n (uniform per 8-lane group: n % 32 == 0)
 #pragma unroll
   for (int c = 0; c < kFlatU; c++) {
     const size_t i0 = base + (size_t)c * 1024;
+    a[c] = b[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (i0 < n) {
+      kn = c + 1;
       a[c] = ld4_nt(g + i0);
       if constexpr (SWIGLU) b[c] = ld4_nt(u + i0);
     }
   }
   bool ok = true;  // every silu argument in the fast range (silu_fast_ok)
+  float y[kFlatU][4];
 #pragma unroll
   for (int c = 0; c < kFlatU; c++) {
-    const size_t i0 = base + (size_t)c * 1024;
-    if (i0 >= n) break;  // whole 8-lane groups leave together
-    float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
+    y[c][0] = a[c].x; y[c][1] = a[c].y; y[c][2] = a[c].z; y[c][3] = a[c].w;
     if constexpr (SWIGLU) {
       const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        ok &= silu_fast_ok(y[k]);
-        y[k] = silu_fast(y[k]) * ub[k];
+        ok &= c >= kn || silu_fast_ok(y[c][k]);
+        y[c][k] = silu_fast(y[c][k]) * ub[k];
       }
     }
-    q8_1_store4<NT>(y, xq, xd, xs, i0);
   }
+  q8_1_store_n<NT, kFlatU, EXACT>(y, xq, xd, xs, base, 1024, kn);
   // A wave with a silu argument outside the fast range (practically never) recomputes its values with the general
   // silu and stores them again; in-range values are unchanged.
   if constexpr (SWIGLU) {
     if (__builtin_expect(__any(!ok), 0)) {
 #pragma unroll
       for (int c = 0; c < kFlatU; c++) {
-        const size_t i0 = base + (size_t)c * 1024;
-        if (i0 >= n) break;
-        float y[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
-        const float ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
+        const float gv[4] = {a[c].x, a[c].y, a[c].z, a[c].w}, ub[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
 #pragma unroll
-        for (int k = 0; k < 4; k++) y[k] = q27_silu(y[k]) * ub[k];
-        q8_1_store4<NT>(y, xq, xd, xs, i0);
+        for (int k = 0; k < 4; k++) y[c][k] = q27_silu(gv[k]) * ub[k];
       }
+      q8_1_store_n<NT, kFlatU, EXACT>(y, xq, xd, xs, base, 1024, kn);
     }
   }
 }
@@ -199,39 +225,42 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
 // wave with any z outside that range (zeros, subnormals, |z| > 60, inf, NaN; practically never) recomputes its
 // heads afterwards with the general silu and stores them again: the same addresses, the later store wins, and
 // the values of in-range lanes are unchanged.
-template <bool NT, int G>
+template <bool NT, int G, bool EXACT>
 __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __restrict__ o, const float* __restrict__ w,
                                                                const float* __restrict__ z, int8_t* __restrict__ xq,
                                                                float* __restrict__ xd, float eps, float* __restrict__ xs,
                                                                int heads) {
-  // G groups of 8 heads per workgroup, all of their o / z loads issued before any head is processed
+  // G groups of 8 heads per workgroup, all of their o / z loads issued before any head is processed; head g of this
+  // 32-lane half is head0 + 8 g, so its values sit 1024 after those of head g - 1
   const int p = threadIdx.x & 31;
   const int off = 32 * (p >> 3) + block_offset(p);
+  const int head0 = blockIdx.x * G * 8 + (threadIdx.x >> 5);
   const float4 wv = ld4(w + off);
   const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
   float4 zv[G], ov[G];
+  int kn = 0;  // heads of this 32-lane half inside `heads`
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    const int head = (blockIdx.x * G + g) * 8 + (threadIdx.x >> 5);
+    const int head = head0 + 8 * g;
+    zv[g] = ov[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (head < heads) {  // uniform per 32-lane half
+      kn = g + 1;
       const size_t i0 = (size_t)head * 128 + off;
       zv[g] = ld4_nt(z + i0);  // z first: silu(z) is computed first
       ov[g] = ld4_nt(o + i0);
     }
   }
+  float y[G][4], sc[G];
+  bool ok = true;
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    const int head = (blockIdx.x * G + g) * 8 + (threadIdx.x >> 5);
-    if (head >= heads) break;  // whole 32-lane halves leave together
-    const size_t i0 = (size_t)head * 128 + off;
     const float v[4] = {ov[g].x, ov[g].y, ov[g].z, ov[g].w};
     const float zz[4] = {zv[g].x, zv[g].y, zv[g].z, zv[g].w};
     float gz[4];
-    bool ok = true;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       gz[c] = silu_fast(zz[c]);
-      ok &= silu_fast_ok(zz[c]);
+      ok &= g >= kn || silu_fast_ok(zz[c]);
     }
     float s[4];
 #pragma unroll
@@ -240,16 +269,21 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __re
     tsum = tsum + 0.0f;  // the reference adds the zero lanes 4..31 (xor 16, 8, 4 steps); x + 0 == x for x >= +0
     tsum += lane_xor<16>(tsum);
     tsum += lane_xor<8>(tsum);
-    const float scale = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
-    float y[4];
+    sc[g] = 1.0f / __builtin_sqrtf(tsum / 128.0f + eps);
 #pragma unroll
-    for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * gz[c];
-    q8_1_store4<NT>(y, xq, xd, xs, i0);
-    if (__builtin_expect(__any(!ok), 0)) {
+    for (int c = 0; c < 4; c++) y[g][c] = (sc[g] * v[c] * ww[c]) * gz[c];
+  }
+  const size_t i0 = (size_t)head0 * 128 + off;
+  q8_1_store_n<NT, G, EXACT>(y, xq, xd, xs, i0, 1024, kn);
+  if (__builtin_expect(__any(!ok), 0)) {
 #pragma unroll
-      for (int c = 0; c < 4; c++) y[c] = (scale * v[c] * ww[c]) * q27_silu(zz[c]);
-      q8_1_store4<NT>(y, xq, xd, xs, i0);
+    for (int g = 0; g < G; g++) {
+      const float v[4] = {ov[g].x, ov[g].y, ov[g].z, ov[g].w};
+      const float zz[4] = {zv[g].x, zv[g].y, zv[g].z, zv[g].w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) y[g][c] = (sc[g] * v[c] * ww[c]) * q27_silu(zz[c]);
     }
+    q8_1_store_n<NT, G, EXACT>(y, xq, xd, xs, i0, 1024, kn);
   }
 }
 
@@ -318,8 +352,13 @@ int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* 
                 int8_t* xq, float* xd, float* xs, int rows, q27h_stream_t s, const uint8_t* wown = nullptr,
                 const uint8_t* wrecv = nullptr, int qb_shift = 0) {
   if (rows == 0) return Q27H_OK;
-  hipLaunchKernelGGL(row_norm_q8_kernel<MODE>, dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h, xq, xd,
-                     xs, wown, wrecv, qb_shift);
+  // up to kLatencyRows rows a launch is latency-bound (one workgroup per row, a few per chip): branch-free quotients
+  if (rows <= kLatencyRows)
+    hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
+                       xq, xd, xs, wown, wrecv, qb_shift);
+  else
+    hipLaunchKernelGGL((row_norm_q8_kernel<MODE, false>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps,
+                       h, xq, xd, xs, wown, wrecv, qb_shift);
   return check_launch(fn);
 }
 
@@ -331,12 +370,16 @@ int launch_flat(const char* fn, bool swiglu, const float* g, const float* u, int
     return fail(Q27H_ERR_ARG, std::string(fn) + ": inputs need 16-byte and xq 4-byte alignment");
   const int U = swiglu ? kSwigluU : kQuantU;
   const size_t blocks = (n + U * 1024 - 1) / (U * 1024);
-  if (swiglu)
-    hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU, kSwigluNT>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd,
-                       xs, n);
+  const bool lat = n <= (size_t)kLatencyRows * kRowN;  // a few workgroups per chip: latency-bound
+  const dim3 grid((unsigned)blocks), block(256);
+  if (swiglu && lat)
+    hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU, kSwigluNT, true>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
+  else if (swiglu)
+    hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU, kSwigluNT, false>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
+  else if (lat)
+    hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU, kQuantNT, true>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
   else
-    hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU, kQuantNT>), dim3((unsigned)blocks), dim3(256), 0, stream_of(s), g, u, xq, xd,
-                       xs, n);
+    hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU, kQuantNT, false>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
   return check_launch(fn);
 }
 
@@ -407,8 +450,13 @@ extern "C" int q27h_gated_rmsnorm_q8(const float* o, const float* w, const float
   if (!o || !w || !z || !xq || !xd) return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: null pointer");
   if (!aligned16(o) || !aligned16(w) || !aligned16(z) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: o, w, z need 16-byte and xq 4-byte alignment");
-  hipLaunchKernelGGL((gated_rmsnorm_q8_kernel<kGatedNT, kGatedG>), dim3((heads + 8 * kGatedG - 1) / (8 * kGatedG)), dim3(256),
-                     0, stream_of(s), o, w, z, xq, xd, eps, xs, heads);
+  const dim3 grid((heads + 8 * kGatedG - 1) / (8 * kGatedG)), block(256);
+  if (heads <= 8 * kLatencyRows)  // decode: a few workgroups per chip, latency-bound
+    hipLaunchKernelGGL((gated_rmsnorm_q8_kernel<kGatedNT, kGatedG, true>), grid, block, 0, stream_of(s), o, w, z, xq, xd, eps,
+                       xs, heads);
+  else
+    hipLaunchKernelGGL((gated_rmsnorm_q8_kernel<kGatedNT, kGatedG, false>), grid, block, 0, stream_of(s), o, w, z, xq, xd, eps,
+                       xs, heads);
   return check_launch("gated_rmsnorm_q8");
 }
 

@@ -49,6 +49,21 @@ __device__ __forceinline__ float lane_xor32(float v) {
 // and stores of the 8 lanes still cover the block's 128 bytes exactly.
 __device__ __forceinline__ int quad_of_lane(int q) { return q < 4 ? q : 11 - q; }
 // Offset (in values) of this thread's four values inside its group's 32-value block.
+// Ends a block of loads: the compiler may not move any instruction across it, so every load above is issued
+// before the first use of any of them (otherwise the scheduler hoists a use of the first value between the loads and
+// the waitcnt it needs holds back the remaining loads by a full memory round trip).
+__device__ __forceinline__ void loads_issued() { __builtin_amdgcn_sched_barrier(0); }
+// Makes the listed kernel arguments live in SGPRs at this point. Placed at kernel entry it turns the compiler's
+// deferred kernarg loads (each a dependent round trip to the kernarg buffer after the launch's cache invalidation)
+// into one batch of scalar loads issued together.
+template <typename T>
+__device__ __forceinline__ void arg_now(T a) {
+  asm volatile("" ::"s"(a));
+}
+template <typename... A>
+__device__ __forceinline__ void args_now(A... a) {
+  (arg_now(a), ...);
+}
 __device__ __forceinline__ int block_offset(int lane) { return 4 * quad_of_lane(lane & 7); }
 
 // The reference's warp_sum (xor 16, 8, 4, 2, 1 over the 32 lanes of a lane group).
@@ -275,6 +290,29 @@ __device__ __forceinline__ float div127(float amax) {
   return amax == __builtin_huge_valf() ? amax : q1;
 }
 
+// roundf(y / d) (q = 0 when d == 0) for finite d >= 0 with |y| <= 127 d, branch-free: d and y are first scaled by
+// the same power of two (exact; the quotient is unchanged) so that d lies in [0.5, 1), then the quotient is formed
+// with the steps of the IEEE division sequence (reciprocal refined by one fma step, two fma residual corrections).
+// With d in [0.5, 1) and |y / d| <= 128 none of the cases in which that sequence pre-scales its operands can arise
+// except a numerator below 2^-103, whose quotient rounds to 0 either way; so the result is the correctly rounded
+// quotient, then rounded half away from zero. Returns false when d is NaN or infinite (the caller then takes the
+// IEEE quotient).
+__device__ __forceinline__ bool q8_quot4_exact(const float (&y)[4], float d, int (&q)[4]) {
+  const int s = -__builtin_amdgcn_frexp_expf(d);
+  const float dn = __builtin_amdgcn_ldexpf(d, s);
+  const float r = __builtin_amdgcn_rcpf(dn);
+  const float r1 = __builtin_fmaf(__builtin_fmaf(-dn, r, 1.0f), r, r);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float yn = __builtin_amdgcn_ldexpf(y[c], s);
+    const float q0 = yn * r1;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-dn, q0, yn), r1, q0);
+    const float q2 = __builtin_fmaf(__builtin_fmaf(-dn, q1, yn), r1, q1);
+    q[c] = d == 0.0f ? 0 : (int)__builtin_roundf(q2);
+  }
+  return d <= 0x1.fffffep127f;
+}
+
 // roundf(y / d) for |y| <= 127 d (the q8_1 rule of src/common.cuh:76; q = 0 when d == 0), four values at a time.
 // For 2^-126 <= d <= 2^126, a = y * rcp(d) (v_rcp_f32, 1 ulp) is within 127 * 2^-22 < 3.1e-5 of the exact quotient,
 // so unless a lies within 2^-12 of a half-integer it rounds to the same integer as the correctly rounded quotient,
@@ -326,6 +364,68 @@ __device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restr
     for (int c = 0; c < 4; c++) u[c] = u[c] + lane_xor<1>(u[c]);
     const float tot = (u[0] + u[2]) + (u[1] + u[3]);
     if ((i0 & 15) == 0) st_f32<NT>(xs + (i0 >> 4), tot);
+  }
+}
+
+// q8_1_store4 for K blocks at once (the lane's values of block k are flat indices i0 + k * stride .. + 3; blocks
+// k >= kn are not stored, kn uniform per 8-lane group). Same results as K calls of q8_1_store4; the K dependent
+// chains (amax exchanges, d, quotients, block sums) are formed side by side, and each kind of store is one guarded
+// group. EXACT: the quotients by q8_quot4_exact (branch-free, about 7 more operations per value: for latency-bound
+// launches, where a wave would otherwise often wait on a fallback); else q8_round_div4 (fewest operations on
+// average: for throughput-bound launches).
+template <bool NT, int K, bool EXACT>
+__device__ __forceinline__ void q8_1_store_n(const float (&y)[K][4], int8_t* __restrict__ xq, float* __restrict__ xd,
+                                             float* __restrict__ xs, size_t i0, size_t stride, int kn = K) {
+  float d[K];
+#pragma unroll
+  for (int k = 0; k < K; k++) {
+    float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(y[k][0]), __builtin_fabsf(y[k][1])),
+                                 __builtin_fmaxf(__builtin_fabsf(y[k][2]), __builtin_fabsf(y[k][3])));
+    amax = __builtin_fmaxf(amax, lane_xor<7>(amax));
+    amax = __builtin_fmaxf(amax, lane_xor<2>(amax));
+    amax = __builtin_fmaxf(amax, lane_xor<1>(amax));
+    d[k] = div127(amax);
+  }
+  int q[K][4];
+  if constexpr (EXACT) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < K; k++) ok &= q8_quot4_exact(y[k], d[k], q[k]);
+    if (__builtin_expect(!ok, 0)) {  // a NaN or infinite block scale
+#pragma unroll
+      for (int k = 0; k < K; k++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[k][c] = d[k] == 0.0f ? 0 : (int)__builtin_roundf(y[k][c] / d[k]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; k++) q8_round_div4(y[k], d[k], q[k]);
+  }
+  float tot[K];
+  if (xs) {
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+      float u[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) u[c] = y[k][c] + lane_xor<2>(y[k][c]);
+#pragma unroll
+      for (int c = 0; c < 4; c++) u[c] = u[c] + lane_xor<1>(u[c]);
+      tot[k] = (u[0] + u[2]) + (u[1] + u[3]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < K; k++)
+    if (k < kn) st_u32<NT>(xq + i0 + k * stride, pack4_i8(q[k][0], q[k][1], q[k][2], q[k][3]));
+  if ((i0 & 31) == 0) {
+#pragma unroll
+    for (int k = 0; k < K; k++)
+      if (k < kn) st_f32<NT>(xd + ((i0 + k * stride) >> 5), fp16_round(d[k]));
+  }
+  if (xs && (i0 & 15) == 0) {
+#pragma unroll
+    for (int k = 0; k < K; k++)
+      if (k < kn) st_f32<NT>(xs + ((i0 + k * stride) >> 4), tot[k]);
   }
 }
 
