@@ -61,7 +61,10 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   const int t = threadIdx.x;
   const size_t row = blockIdx.x;
   const int off = 32 * (t >> 3) + block_offset(t);  // this thread's 4 values in each 1024-value slice
-  const size_t base = row * kRowN + off;
+  const size_t rb = row * kRowN;  // row-relative indices below: 32-bit address arithmetic
+  float* const xr = x + rb;
+  const float* const pr = partial + rb;
+  const uint16_t* const rr = recv + rb;
   // every load of the row first (x, the added operands, w), one memory round trip
   float v[5][4];
   float4 wv[5];
@@ -73,16 +76,16 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   uint16_t odb[NQ], rdb[NQ];
 #pragma unroll
   for (int k = 0; k < 5; k++) {
-    const float4 a = ld4_row(x + base + k * 1024);
+    const float4 a = ld4_row(xr + off + k * 1024);
     v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
   }
   if constexpr (MODE == kAddPartial || MODE == kAddBf16Recv) {
 #pragma unroll
-    for (int k = 0; k < 5; k++) pv4[k] = ld4_row(partial + base + k * 1024);
+    for (int k = 0; k < 5; k++) pv4[k] = ld4_row(pr + off + k * 1024);
   }
   if constexpr (MODE == kAddBf16Recv) {
 #pragma unroll
-    for (int k = 0; k < 5; k++) rv2[k] = *(const uint2*)(recv + base + k * 1024);
+    for (int k = 0; k < 5; k++) rv2[k] = *(const uint2*)(rr + off + k * 1024);
   }
   if constexpr (MODE == kAddQ8Wire) {
     const size_t rb = kRowN + ((size_t)2 * kRowN >> qb_shift);
@@ -110,7 +113,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
         const float a = od * (float)(int8_t)(oq[k] >> (8 * c)), b = rd * (float)(int8_t)(rq[k] >> (8 * c));
         v[k][c] = v[k][c] + (a + b);
       }
-      st4<kRowNT>(x + base + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
+      st4<kRowNT>(xr + off + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
     }
   } else if constexpr (MODE != kPlain) {
 #pragma unroll
@@ -126,7 +129,7 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 #pragma unroll
         for (int c = 0; c < 4; c++) v[k][c] = v[k][c] + (bf16_round(pv[c]) + rv[c]);
       }
-      st4<kRowNT>(x + base + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
+      st4<kRowNT>(xr + off + k * 1024, v[k][0], v[k][1], v[k][2], v[k][3]);
     }
   }
   // per virtual thread: t = 0; t += v[k]^2 for k = 0..4 (src/ops.cu:96-98)
@@ -152,9 +155,9 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   }
   if (h) {
 #pragma unroll
-    for (int k = 0; k < 5; k++) st4<kRowNT>(h + base + k * 1024, y[k][0], y[k][1], y[k][2], y[k][3]);
+    for (int k = 0; k < 5; k++) st4<kRowNT>(h + rb + off + k * 1024, y[k][0], y[k][1], y[k][2], y[k][3]);
   }
-  q8_1_store_n<kRowNT, 5, EXACT>(y, xq, xd, xs, base, 1024);
+  q8_1_store_n<kRowNT, 5, EXACT>(y, xq + rb, xd + rb / 32, xs ? xs + rb / 16 : nullptr, off, 1024);
 }
 
 // ---------------------------------------------------------------- flat q8_1 producers
@@ -173,7 +176,12 @@ template <bool SWIGLU, int kFlatU, bool NT, bool EXACT>
 __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                       int8_t* __restrict__ xq, float* __restrict__ xd,
                                                       float* __restrict__ xs, size_t n) {
-  const size_t base = (size_t)blockIdx.x * (kFlatU * 1024) + 32 * (threadIdx.x >> 3) + block_offset(threadIdx.x);
+  const size_t wb = (size_t)blockIdx.x * (kFlatU * 1024);  // this workgroup's first value
+  const int off = 32 * (threadIdx.x >> 3) + block_offset(threadIdx.x);
+  const size_t base = wb + off;
+  int8_t* const xq_w = xq + wb;
+  float* const xd_w = xd + wb / 32;
+  float* const xs_w = xs ? xs + wb / 16 : nullptr;
   float4 a[kFlatU], b[kFlatU];
   int kn = 0;  // chunks of this lane inside n (uniform per 8-lane group: n % 32 == 0)
 #pragma unroll
@@ -200,7 +208,7 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
       }
     }
   }
-  q8_1_store_n<NT, kFlatU, EXACT>(y, xq, xd, xs, base, 1024, kn);
+  q8_1_store_n<NT, kFlatU, EXACT>(y, xq_w, xd_w, xs_w, off, 1024, kn);
   // A wave with a silu argument outside the fast range (practically never) recomputes its values with the general
   // silu and stores them again; in-range values are unchanged.
   if constexpr (SWIGLU) {
@@ -211,7 +219,7 @@ __global__ void __launch_bounds__(256) flat_q8_kernel(const float* __restrict__ 
 #pragma unroll
         for (int k = 0; k < 4; k++) y[c][k] = q27_silu(gv[k]) * ub[k];
       }
-      q8_1_store_n<NT, kFlatU, EXACT>(y, xq, xd, xs, base, 1024, kn);
+      q8_1_store_n<NT, kFlatU, EXACT>(y, xq_w, xd_w, xs_w, off, 1024, kn);
     }
   }
 }
@@ -273,8 +281,12 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __re
 #pragma unroll
     for (int c = 0; c < 4; c++) y[g][c] = (sc[g] * v[c] * ww[c]) * gz[c];
   }
-  const size_t i0 = (size_t)head0 * 128 + off;
-  q8_1_store_n<NT, G, EXACT>(y, xq, xd, xs, i0, 1024, kn);
+  const size_t wb = (size_t)blockIdx.x * G * 8 * 128;  // this workgroup's first value
+  const int i0 = (threadIdx.x >> 5) * 128 + off;
+  int8_t* const xq_w = xq + wb;
+  float* const xd_w = xd + wb / 32;
+  float* const xs_w = xs ? xs + wb / 16 : nullptr;
+  q8_1_store_n<NT, G, EXACT>(y, xq_w, xd_w, xs_w, i0, 1024, kn);
   if (__builtin_expect(__any(!ok), 0)) {
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -283,7 +295,7 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_q8_kernel(const float* __re
 #pragma unroll
       for (int c = 0; c < 4; c++) y[g][c] = (sc[g] * v[c] * ww[c]) * q27_silu(zz[c]);
     }
-    q8_1_store_n<NT, G, EXACT>(y, xq, xd, xs, i0, 1024, kn);
+    q8_1_store_n<NT, G, EXACT>(y, xq_w, xd_w, xs_w, i0, 1024, kn);
   }
 }
 
@@ -353,6 +365,7 @@ int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* 
                 const uint8_t* wrecv = nullptr, int qb_shift = 0) {
   if (rows == 0) return Q27H_OK;
   // up to kLatencyRows rows a launch is latency-bound (one workgroup per row, a few per chip): branch-free quotients
+  // (a 1024-thread form with 5 values per lane, the reference's layout, measured slower: 4.0 against 3.3 us per node)
   if (rows <= kLatencyRows)
     hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
                        xq, xd, xs, wown, wrecv, qb_shift);
@@ -368,16 +381,17 @@ int launch_flat(const char* fn, bool swiglu, const float* g, const float* u, int
   if (!g || !xq || !xd || (swiglu && !u)) return fail(Q27H_ERR_ARG, std::string(fn) + ": null pointer");
   if (!aligned16(g) || (swiglu && !aligned16(u)) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, std::string(fn) + ": inputs need 16-byte and xq 4-byte alignment");
-  const int U = swiglu ? kSwigluU : kQuantU;
-  const size_t blocks = (n + U * 1024 - 1) / (U * 1024);
-  const bool lat = n <= (size_t)kLatencyRows * kRowN;  // a few workgroups per chip: latency-bound
-  const dim3 grid((unsigned)blocks), block(256);
+  // a launch of a few workgroups per chip is latency-bound: one 1024-value chunk per workgroup (the shortest chain
+  // per lane) and branch-free quotients
+  const bool lat = n <= (size_t)kLatencyRows * kRowN;
+  const int U = lat ? 1 : swiglu ? kSwigluU : kQuantU;
+  const dim3 grid((unsigned)((n + U * 1024 - 1) / (U * 1024))), block(256);
   if (swiglu && lat)
-    hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU, kSwigluNT, true>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
+    hipLaunchKernelGGL((flat_q8_kernel<true, 1, kSwigluNT, true>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
   else if (swiglu)
     hipLaunchKernelGGL((flat_q8_kernel<true, kSwigluU, kSwigluNT, false>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
   else if (lat)
-    hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU, kQuantNT, true>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
+    hipLaunchKernelGGL((flat_q8_kernel<false, 1, kQuantNT, true>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
   else
     hipLaunchKernelGGL((flat_q8_kernel<false, kQuantU, kQuantNT, false>), grid, block, 0, stream_of(s), g, u, xq, xd, xs, n);
   return check_launch(fn);
@@ -450,13 +464,12 @@ extern "C" int q27h_gated_rmsnorm_q8(const float* o, const float* w, const float
   if (!o || !w || !z || !xq || !xd) return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: null pointer");
   if (!aligned16(o) || !aligned16(w) || !aligned16(z) || !aligned4(xq))
     return fail(Q27H_ERR_ARG, "gated_rmsnorm_q8: o, w, z need 16-byte and xq 4-byte alignment");
-  const dim3 grid((heads + 8 * kGatedG - 1) / (8 * kGatedG)), block(256);
-  if (heads <= 8 * kLatencyRows)  // decode: a few workgroups per chip, latency-bound
-    hipLaunchKernelGGL((gated_rmsnorm_q8_kernel<kGatedNT, kGatedG, true>), grid, block, 0, stream_of(s), o, w, z, xq, xd, eps,
-                       xs, heads);
+  if (heads <= 8 * kLatencyRows)  // decode: a few workgroups per chip, latency-bound; one head per 32-lane half
+    hipLaunchKernelGGL((gated_rmsnorm_q8_kernel<kGatedNT, 1, true>), dim3((heads + 7) / 8), dim3(256), 0, stream_of(s), o, w, z,
+                       xq, xd, eps, xs, heads);
   else
-    hipLaunchKernelGGL((gated_rmsnorm_q8_kernel<kGatedNT, kGatedG, false>), grid, block, 0, stream_of(s), o, w, z, xq, xd, eps,
-                       xs, heads);
+    hipLaunchKernelGGL((gated_rmsnorm_q8_kernel<kGatedNT, kGatedG, false>), dim3((heads + 8 * kGatedG - 1) / (8 * kGatedG)),
+                       dim3(256), 0, stream_of(s), o, w, z, xq, xd, eps, xs, heads);
   return check_launch("gated_rmsnorm_q8");
 }
 

@@ -41,14 +41,7 @@ __device__ __forceinline__ float lane_xor32(float v) {
   return __builtin_bit_cast(float, (__lane_id() & 32) ? (int)pr[0] : (int)pr[1]);
 }
 
-// ---------------------------------------------------------------- lane layout of a 32-value block
-// Eight lanes hold one block of 32 consecutive values, four per lane. Lane q (= lane & 7) holds the four values at
-// 4 * quad_of_lane(q): lanes 0..3 take quads 0..3 and lanes 4..7 quads 7..4. With this order the reference's
-// butterfly over the block's 32 virtual lanes (xor 16, 8, 4, 2, 1) is lane xor 7 (row_half_mirror), lane xor 2,
-// lane xor 1 (quad permutes) and then the lane's own value pairs: DPP operands that fold into the adds. The loads
-// and stores of the 8 lanes still cover the block's 128 bytes exactly.
-__device__ __forceinline__ int quad_of_lane(int q) { return q < 4 ? q : 11 - q; }
-// Offset (in values) of this thread's four values inside its group's 32-value block.
+// ---------------------------------------------------------------- scheduling
 // Ends a block of loads: the compiler may not move any instruction across it, so every load above is issued
 // before the first use of any of them (otherwise the scheduler hoists a use of the first value between the loads and
 // the waitcnt it needs holds back the remaining loads by a full memory round trip).
@@ -64,6 +57,15 @@ template <typename... A>
 __device__ __forceinline__ void args_now(A... a) {
   (arg_now(a), ...);
 }
+
+// ---------------------------------------------------------------- lane layout of a 32-value block
+// Eight lanes hold one block of 32 consecutive values, four per lane. Lane q (= lane & 7) holds the four values at
+// 4 * quad_of_lane(q): lanes 0..3 take quads 0..3 and lanes 4..7 quads 7..4. With this order the reference's
+// butterfly over the block's 32 virtual lanes (xor 16, 8, 4, 2, 1) is lane xor 7 (row_half_mirror), lane xor 2,
+// lane xor 1 (quad permutes) and then the lane's own value pairs: DPP operands that fold into the adds. The loads
+// and stores of the 8 lanes still cover the block's 128 bytes exactly.
+__device__ __forceinline__ int quad_of_lane(int q) { return q < 4 ? q : 11 - q; }
+// Offset (in values) of this thread's four values inside its group's 32-value block.
 __device__ __forceinline__ int block_offset(int lane) { return 4 * quad_of_lane(lane & 7); }
 
 // The reference's warp_sum (xor 16, 8, 4, 2, 1 over the 32 lanes of a lane group).
@@ -290,27 +292,26 @@ __device__ __forceinline__ float div127(float amax) {
   return amax == __builtin_huge_valf() ? amax : q1;
 }
 
-// roundf(y / d) (q = 0 when d == 0) for finite d >= 0 with |y| <= 127 d, branch-free: d and y are first scaled by
-// the same power of two (exact; the quotient is unchanged) so that d lies in [0.5, 1), then the quotient is formed
-// with the steps of the IEEE division sequence (reciprocal refined by one fma step, two fma residual corrections).
-// With d in [0.5, 1) and |y / d| <= 128 none of the cases in which that sequence pre-scales its operands can arise
-// except a numerator below 2^-103, whose quotient rounds to 0 either way; so the result is the correctly rounded
-// quotient, then rounded half away from zero. Returns false when d is NaN or infinite (the caller then takes the
-// IEEE quotient).
-__device__ __forceinline__ bool q8_quot4_exact(const float (&y)[4], float d, int (&q)[4]) {
-  const int s = -__builtin_amdgcn_frexp_expf(d);
-  const float dn = __builtin_amdgcn_ldexpf(d, s);
-  const float r = __builtin_amdgcn_rcpf(dn);
-  const float r1 = __builtin_fmaf(__builtin_fmaf(-dn, r, 1.0f), r, r);
+// roundf(y / d) (q = 0 when d == 0) for |y| <= 127 d, branch-free: the quotient is formed with the steps of the IEEE
+// division sequence (reciprocal refined by one fma step, two fma residual corrections), which give the correctly
+// rounded quotient unless the sequence would have to pre-scale its operands. For 2^-100 <= d <= 2^100 and
+// |y / d| >= 1/2 it never would, and a smaller quotient rounds to 0 either way; the result is then rounded half away
+// from zero. Returns false for any other d except 0 (subnormal, tiny, huge, infinite or NaN scales: the caller then
+// takes the IEEE quotient).
+template <int N>
+__device__ __forceinline__ bool q8_quot_exact(const float (&y)[N], float d, int (&q)[N]) {
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float r1 = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const float yn = __builtin_amdgcn_ldexpf(y[c], s);
-    const float q0 = yn * r1;
-    const float q1 = __builtin_fmaf(__builtin_fmaf(-dn, q0, yn), r1, q0);
-    const float q2 = __builtin_fmaf(__builtin_fmaf(-dn, q1, yn), r1, q1);
-    q[c] = d == 0.0f ? 0 : (int)__builtin_roundf(q2);
+  for (int c = 0; c < N; c++) {
+    const float q0 = y[c] * r1;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-d, q0, y[c]), r1, q0);
+    const float q2 = __builtin_fmaf(__builtin_fmaf(-d, q1, y[c]), r1, q1);
+    int qi = (int)__builtin_roundf(q2);
+    asm volatile("" : "+v"(qi));  // formed unconditionally: no branch around the quotient for d == 0
+    q[c] = d == 0.0f ? 0 : qi;
   }
-  return d <= 0x1.fffffep127f;
+  return (d == 0.0f) | ((d >= 0x1p-100f) & (d <= 0x1p100f));
 }
 
 // roundf(y / d) for |y| <= 127 d (the q8_1 rule of src/common.cuh:76; q = 0 when d == 0), four values at a time.
@@ -338,44 +339,19 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
 
-// q8_1 of a 32-value block held by the 8 lanes of a group in the block layout above (the lane's values are flat
-// indices i0 .. i0 + 3): amax over the block, d = amax / 127, q = roundf(y / d) (0 when amax == 0), xd = fp16(d)
-// as f32, and the optional per-16 sums of the unquantized values in the reference's butterfly order (xor 8, 4, 2, 1
-// over the 16 virtual lanes = lane xor 2, lane xor 1, then value pairs (0,2)(1,3), then (0,1)); the block's first
-// 16 values sit in lanes 0..3 of the group and the last 16 in lanes 4..7.
-template <bool NT = false>
-__device__ __forceinline__ void q8_1_store4(const float (&y)[4], int8_t* __restrict__ xq, float* __restrict__ xd,
-                                            float* __restrict__ xs, size_t i0) {
-  float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(y[0]), __builtin_fabsf(y[1])),
-                               __builtin_fmaxf(__builtin_fabsf(y[2]), __builtin_fabsf(y[3])));
-  amax = __builtin_fmaxf(amax, lane_xor<7>(amax));
-  amax = __builtin_fmaxf(amax, lane_xor<2>(amax));
-  amax = __builtin_fmaxf(amax, lane_xor<1>(amax));
-  const float d = div127(amax);
-  int q[4];
-  q8_round_div4(y, d, q);
-  st_u32<NT>(xq + i0, pack4_i8(q[0], q[1], q[2], q[3]));
-  if ((i0 & 31) == 0) st_f32<NT>(xd + (i0 >> 5), fp16_round(d));
-  if (xs) {
-    float u[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) u[c] = y[c] + lane_xor<2>(y[c]);
-#pragma unroll
-    for (int c = 0; c < 4; c++) u[c] = u[c] + lane_xor<1>(u[c]);
-    const float tot = (u[0] + u[2]) + (u[1] + u[3]);
-    if ((i0 & 15) == 0) st_f32<NT>(xs + (i0 >> 4), tot);
-  }
-}
-
-// q8_1_store4 for K blocks at once (the lane's values of block k are flat indices i0 + k * stride .. + 3; blocks
-// k >= kn are not stored, kn uniform per 8-lane group). Same results as K calls of q8_1_store4; the K dependent
-// chains (amax exchanges, d, quotients, block sums) are formed side by side, and each kind of store is one guarded
-// group. EXACT: the quotients by q8_quot4_exact (branch-free, about 7 more operations per value: for latency-bound
-// launches, where a wave would otherwise often wait on a fallback); else q8_round_div4 (fewest operations on
-// average: for throughput-bound launches).
+// q8_1 of K 32-value blocks held by the 8 lanes of a group in the block layout above: the lane's values of block k
+// are the flat indices i0 + k * stride .. + 3 of the arrays xq (values), xd (one scale per 32) and xs (one sum per 16),
+// which the caller offsets to a 32-aligned base so that the indices stay 32-bit; blocks k >= kn are not stored (kn
+// uniform per 8-lane group). Per block: amax, d = amax / 127, q = roundf(y / d) (0 when amax == 0), xd = fp16(d) as
+// f32, and the optional per-16 sums of the unquantized values in the reference's butterfly order (xor 8, 4, 2, 1 over
+// the 16 virtual lanes = lane xor 2, lane xor 1, then value pairs (0,2)(1,3), then (0,1)); the block's first 16
+// values sit in lanes 0..3 of the group and the last 16 in lanes 4..7. The K dependent chains are formed side by side
+// and each kind of store is one guarded group. EXACT: the quotients by q8_quot_exact (branch-free, a few more
+// operations per value: for latency-bound launches, where a wave would otherwise often wait on a fallback); else
+// q8_round_div4 (fewest operations on average: for throughput-bound launches).
 template <bool NT, int K, bool EXACT>
 __device__ __forceinline__ void q8_1_store_n(const float (&y)[K][4], int8_t* __restrict__ xq, float* __restrict__ xd,
-                                             float* __restrict__ xs, size_t i0, size_t stride, int kn = K) {
+                                             float* __restrict__ xs, int i0, int stride, int kn = K) {
   float d[K];
 #pragma unroll
   for (int k = 0; k < K; k++) {
@@ -390,8 +366,8 @@ __device__ __forceinline__ void q8_1_store_n(const float (&y)[K][4], int8_t* __r
   if constexpr (EXACT) {
     bool ok = true;
 #pragma unroll
-    for (int k = 0; k < K; k++) ok &= q8_quot4_exact(y[k], d[k], q[k]);
-    if (__builtin_expect(!ok, 0)) {  // a NaN or infinite block scale
+    for (int k = 0; k < K; k++) ok &= q8_quot_exact<4>(y[k], d[k], q[k]);
+    if (__builtin_expect(__any(!ok), 0)) {  // a scale outside [2^-100, 2^100]: practically never
 #pragma unroll
       for (int k = 0; k < K; k++) {
 #pragma unroll

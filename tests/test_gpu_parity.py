@@ -129,10 +129,16 @@ def test_quantize_q8_1(q27, oracle, T, ncols, K):
         assert_bits_equal(T.down(got), want, what)
 
 
-def test_q8_rounding_near_half_integers(q27, oracle, T):
-    """Values whose quotient y / d lies on or within a few ulps of k + 0.5: the fast y * (1/d) path must hand these to
-    the IEEE quotient (roundf, ties away from zero), exactly as the oracle rounds them."""
-    say("q8_1 rounding near half-integers")
+# Launches of up to 64 rows of 5120 values take the branch-free exact quotient, larger ones the reciprocal fast path
+# with its IEEE fallback: reps = 1 runs the first, reps = 3 (the same blocks three times over) the second.
+LAT_LIMIT = 64 * E
+
+
+@pytest.mark.parametrize("reps", [1, 3])
+def test_q8_rounding_near_half_integers(q27, oracle, T, reps):
+    """Values whose quotient y / d lies on or within a few ulps of k + 0.5: both quotient paths must round them as the
+    IEEE quotient does (roundf, ties away from zero), exactly as the oracle rounds them."""
+    say(f"q8_1 rounding near half-integers reps={reps}")
     r = cd.rng(123)
     nblk = 4096
     amax = np.exp(r.uniform(-8, 8, nblk)).astype(np.float32)
@@ -141,7 +147,8 @@ def test_q8_rounding_near_half_integers(q27, oracle, T):
     y = ((k + np.float32(0.5)) * d[:, None]).astype(np.float32)
     ulps = r.integers(-3, 4, (nblk, 31)).astype(np.int32)
     y = (y.view(np.int32) + ulps).view(np.float32)  # on the tie and a few ulps either side
-    x = np.concatenate([amax[:, None], y], 1).reshape(-1)  # lane 0 of each block fixes amax (and so d)
+    x = np.tile(np.concatenate([amax[:, None], y], 1).reshape(-1), reps)  # lane 0 of each block fixes amax (and so d)
+    assert (x.size <= LAT_LIMIT) == (reps == 1)
     xq, xd, xs = q8_bufs(T, x.size, True)
     q27.ops.quantize_q8_1(T.up(x), xq, xd, x.size, 1, None, xs)
     oq, od, os_ = oracle.quantize_q8_1(x, x.size, 1, with_xs=True)
@@ -149,10 +156,11 @@ def test_q8_rounding_near_half_integers(q27, oracle, T):
         assert_bits_equal(T.down(got), want, what)
 
 
-def test_q8_tiny_and_huge_scales(q27, oracle, T):
+@pytest.mark.parametrize("reps", [1, 6])
+def test_q8_tiny_and_huge_scales(q27, oracle, T, reps):
     """Blocks whose scale d = amax / 127 is subnormal or tiny (the reciprocal path hands them to the IEEE quotient) or
-    very large, subnormal inputs, and all-zero blocks."""
-    say("q8_1 tiny and huge scales")
+    very large, subnormal inputs, and all-zero blocks, through both quotient paths."""
+    say(f"q8_1 tiny and huge scales reps={reps}")
     r = cd.rng(321)
     nblk = 2048
     e = np.concatenate([r.uniform(-149, -100, nblk // 2), r.uniform(100, 127, nblk // 2)])
@@ -160,7 +168,8 @@ def test_q8_tiny_and_huge_scales(q27, oracle, T):
     y = (r.uniform(-1, 1, (nblk, 31)) * amax[:, None]).astype(np.float32)
     x = np.concatenate([amax[:, None], y], 1)
     x[::7] = 0  # all-zero blocks
-    x = x.reshape(-1)
+    x = np.tile(x.reshape(-1), reps)
+    assert (x.size <= LAT_LIMIT) == (reps == 1)
     xq, xd, xs = q8_bufs(T, x.size, True)
     q27.ops.quantize_q8_1(T.up(x), xq, xd, x.size, 1, None, xs)
     oq, od, os_ = oracle.quantize_q8_1(x, x.size, 1, with_xs=True)
