@@ -172,11 +172,12 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
   }
 }
 
-// Decode (T <= 4, src/ops.cu:288-338): one 128-thread workgroup per head, 32 lanes per token, so the T tokens run
-// side by side. Token t's window is inputs t-3 .. t-1 (the state plane `pin` for negative ones); snapshot plane t
+// Decode (T <= 4, src/ops.cu:288-338): one workgroup per head, 32 lanes per token, so the T tokens run side by side,
+// and a third wave that evaluates the head's T gates (a serial chain of exp, division and log that, on a lane of the
+// conv waves, added 0.6 us to a 4.1 us node). Token t's window is inputs t-3 .. t-1 (the state plane `pin` for negative ones); snapshot plane t
 // receives inputs t-2 .. t. Planes are read before the barrier and written after it, because a snapshot may
 // overwrite plane `pin` while another token still needs it.
-__global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __restrict__ x, const float* __restrict__ cw,
+__global__ void __launch_bounds__(192) gdn_conv_decode_kernel(const float* __restrict__ x, const float* __restrict__ cw,
                                                               float* __restrict__ planes, const int* __restrict__ in_plane,
                                                               float* __restrict__ y, int C, int T, int snapshots,
                                                               int n_norm_heads, float eps, const float* __restrict__ a,
@@ -184,6 +185,12 @@ __global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __res
                                                               const float* __restrict__ dt_bias, float* __restrict__ g,
                                                               float* __restrict__ beta, int H) {
   const int head = blockIdx.x;
+  if (threadIdx.x >= 128) {  // the gate wave: gate_one of token (lane) for a value head, beside the conv waves
+    __syncthreads();         // the conv waves' one barrier (wave-uniform branch, so the counts match)
+    const int lane = threadIdx.x - 128;
+    if (head >= n_norm_heads && lane < T) gate_one(a, b, ssm_a, dt_bias, g, beta, lane, H, head - n_norm_heads);
+    return;
+  }
   const int t = threadIdx.x >> 5, p = threadIdx.x & 31;
   const int cb = head * 128 + l2_lane(p);  // channels cb + 32k
   const bool active = t < T;
@@ -228,7 +235,6 @@ __global__ void __launch_bounds__(128) gdn_conv_decode_kernel(const float* __res
     }
   }
   if (head < n_norm_heads) l2_head_lanes(out, eps);
-  else if (p == 0) gate_one(a, b, ssm_a, dt_bias, g, beta, t, H, head - n_norm_heads);
   float* yr = y + (size_t)t * C + cb;
   yr[0] = out[0]; yr[32] = out[1]; yr[64] = out[2]; yr[96] = out[3];
 }
@@ -332,7 +338,7 @@ extern "C" int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, c
     return e;
   if (T > 4) return fail(Q27H_ERR_SHAPE, "gdn_conv_l2: T must be <= 4 (4 state planes)");
   if (T == 0) return Q27H_OK;
-  hipLaunchKernelGGL(gdn_conv_decode_kernel, dim3(C / 128), dim3(128), 0, stream_of(s), x, w, planes, in_plane, y, C, T,
+  hipLaunchKernelGGL(gdn_conv_decode_kernel, dim3(C / 128), dim3(192), 0, stream_of(s), x, w, planes, in_plane, y, C, T,
                      snapshots, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H);
   return check_launch("gdn_conv_l2");
 }
