@@ -296,7 +296,7 @@ __device__ __forceinline__ float div127(float amax) {
 // division sequence (reciprocal refined by one fma step, two fma residual corrections), which give the correctly
 // rounded quotient unless the sequence would have to pre-scale its operands. For 2^-100 <= d <= 2^100 and
 // |y / d| >= 1/2 it never would, and a smaller quotient rounds to 0 either way; the result is then rounded half away
-// from zero. Returns false for any other d except 0 (subnormal, tiny, huge, infinite or NaN scales: the caller then
+// from zero (|y / d| <= 127 (1 + 2^-22) here). Returns false for any other d except 0 (subnormal, tiny, huge, infinite or NaN scales: the caller then
 // takes the IEEE quotient).
 template <int N>
 __device__ __forceinline__ bool q8_quot_exact(const float (&y)[N], float d, int (&q)[N]) {
@@ -307,7 +307,9 @@ __device__ __forceinline__ bool q8_quot_exact(const float (&y)[N], float d, int 
     const float q0 = y[c] * r1;
     const float q1 = __builtin_fmaf(__builtin_fmaf(-d, q0, y[c]), r1, q0);
     const float q2 = __builtin_fmaf(__builtin_fmaf(-d, q1, y[c]), r1, q1);
-    int qi = (int)__builtin_roundf(q2);
+    // roundf(q2) for |q2| <= 130 (checked against roundf for every float in that range): q2 + copysign(0.5 - 2^-25)
+    // rounds to nearest, then the conversion truncates
+    int qi = (int)(q2 + __builtin_copysignf(0x1.fffffep-2f, q2));
     asm volatile("" : "+v"(qi));  // formed unconditionally: no branch around the quotient for d == 0
     q[c] = d == 0.0f ? 0 : qi;
   }
