@@ -301,7 +301,8 @@ __device__ __forceinline__ float div127(float amax) {
 template <int N>
 __device__ __forceinline__ bool q8_quot_exact(const float (&y)[N], float d, int (&q)[N]) {
   const float r = __builtin_amdgcn_rcpf(d);
-  const float r1 = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+  // d == 0 (then every y is +-0): a zero reciprocal makes every step below exactly +-0, so q = 0 without a select
+  const float r1 = d == 0.0f ? 0.0f : __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
 #pragma unroll
   for (int c = 0; c < N; c++) {
     const float q0 = y[c] * r1;
@@ -309,9 +310,7 @@ __device__ __forceinline__ bool q8_quot_exact(const float (&y)[N], float d, int 
     const float q2 = __builtin_fmaf(__builtin_fmaf(-d, q1, y[c]), r1, q1);
     // roundf(q2) for |q2| <= 130 (checked against roundf for every float in that range): q2 + copysign(0.5 - 2^-25)
     // rounds to nearest, then the conversion truncates
-    int qi = (int)(q2 + __builtin_copysignf(0x1.fffffep-2f, q2));
-    asm volatile("" : "+v"(qi));  // formed unconditionally: no branch around the quotient for d == 0
-    q[c] = d == 0.0f ? 0 : qi;
+    q[c] = (int)(q2 + __builtin_copysignf(0x1.fffffep-2f, q2));
   }
   return (d == 0.0f) | ((d >= 0x1p-100f) & (d <= 0x1p100f));
 }
