@@ -176,8 +176,9 @@ int q27h_qmat_repack(int type, int N, int K, const void* raw, void* buf, q27h_st
  * takes 1, 2 or 4), x as q8_1 activations xq [ncols][K] (16-byte aligned), xd [ncols][K/32]. */
 int q27h_qgemv(int type, int N, int K, const void* buf, const int8_t* xq, const float* xd, float* y, int ncols,
                q27h_stream_t s);
-/* Waves that share one 8-row tile in q27h_qgemv (1, 2 or 4): part of the summation order, a function of N only. */
-int q27h_qgemv_waves(int N, int K);
+/* Waves that share one 8-row tile in a q27h_qgemv launch of ncols columns (1..16; three columns run as launches of two
+ * and one): part of the summation order, a function of the type, K and ncols only. */
+int q27h_qgemv_waves(int type, int K, int ncols);
 
 /* ---------------------------------------------------------------- GGUF reader (src/gguf.h, src/gguf.cpp)
  * Version-3 files only, memory-mapped read-only for the life of the handle; tensor data pointers point into the

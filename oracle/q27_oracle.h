@@ -97,7 +97,7 @@ const uint64_t* q27o_iq2s_grid(void);
 /* ---- decode GEMV over quantized weights (q27_oracle_qgemv.c): raw GGUF rows, q8_1 activations, ncols 1..4.
  * Types: ggml ids 12 (Q4_K), 14 (Q6_K), 21 (IQ3_S), 23 (IQ4_XS). Returns 0, or -1 for a bad shape / type. */
 int q27o_qgemv_block_bytes(int type);
-int q27o_qgemv_waves(int N, int K);
+int q27o_qgemv_waves(int type, int K, int ncols);
 int q27o_qgemv(int type, const uint8_t* raw, int N, int K, const int8_t* xq, const float* xd, float* y, int ncols);
 
 #ifdef __cplusplus

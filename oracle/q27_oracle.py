@@ -56,7 +56,7 @@ _SIGS = {
     "q27o_get_rows_q8_0": (None, [_p, _i64, _p, _i, _p, _i, _p]),
     "q27o_iq2s_grid": (C.POINTER(C.c_uint64), []),
     "q27o_qgemv_block_bytes": (_i, [_i]),
-    "q27o_qgemv_waves": (_i, [_i, _i]),
+    "q27o_qgemv_waves": (_i, [_i, _i, _i]),
     "q27o_qgemv": (_i, [_i, _p, _i, _i, _p, _p, _p, _i]),
     "q27o_to_bf16": (None, [_p, _p, C.c_size_t]),
     "q27o_gemv_bf16_pair": (None, [_p, _p, _p, _p, _p, _i, _i, _i]),
@@ -322,8 +322,8 @@ def qgemv(type_, raw, N, K, xq, xd, ncols):
     return y.reshape(ncols, N)
 
 
-def qgemv_waves(N, K):
-    return int(lib().q27o_qgemv_waves(N, K))
+def qgemv_waves(type_, K, ncols):
+    return int(lib().q27o_qgemv_waves(type_, K, ncols))
 
 
 def gdn_step(q, k, v, stride, g, beta, planes, in_plane, H, HK, T, scale, snapshots, flip, parts=None):

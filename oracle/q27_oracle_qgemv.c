@@ -6,10 +6,10 @@
  * block's quants with the 32 int8 activations (llama.cpp vecdotq semantics), turned into a float contribution
  * t(b, s) with the reference's float expression of that type. Only the summation order of the t is this build's own
  * (the reference's depends on the SM count through its split-K choice, src/qgemv.cu:743-753):
- *   - W "waves" per 8-row tile (q27o_qgemv_waves), 64 lanes each, lane = 8 lb + s; slot g = 8 w + lb takes the
+ *   - W "waves" per 8-row tile (q27o_qgemv_waves of the type, K and the launch's column count), 64 lanes each, lane = 8 lb + s; slot g = 8 w + lb takes the
  *     blocks g, g + 8 W, g + 16 W, ... in ascending order: acc = 0, acc = acc + t(b, s);
  *   - the 64 lane sums of a wave are added as an xor butterfly (lane xor 32, 16, 8, 4, 2, 1);
- *   - the wave sums are added in wave order: ((P0 + P1) + P2) + P3.
+ *   - the wave sums are added in wave order: ((P0 + P1) + P2) + ...
  * The GPU kernel (qwen27-engine_amd/csrc/qgemv.hip) adds the same operands in the same order.
  * Block formats: ggml block_q2_K / q4_K / q6_K / iq2_xxs / iq2_xs / iq2_s / iq3_xxs / iq3_s / iq4_xs / iq1_m
  * (ggml-common.h), the dequantization order of src/requant.cpp:68-114 (Q6_K, Q4_K) and ggml's dequantize_row_*; the
@@ -77,12 +77,14 @@ int q27o_qgemv_block_bytes(int type) {
   }
 }
 
-/* Waves per 8-row tile: a function of the shape only (ceil(K / 2048), at most 4), so results do not depend on the
- * device. */
-int q27o_qgemv_waves(int N, int K) {
-  (void)N;
+/* Waves per 8-row tile: a function of the type, K and the column count only, so results do not depend on the device.
+ * One column, and two for all types but IQ3_XXS / IQ3_S / IQ1_M: ceil(K / 2048) up to K = 32768 (at most 16);
+ * otherwise at most 4; K > 32768: 4. */
+int q27o_qgemv_waves(int type, int K, int ncols) {
   const int w = (K / 256 + 7) / 8;
-  return w < 1 ? 1 : w > 4 ? 4 : w;
+  const int wide = ncols == 1 || (ncols == 2 && type != 18 && type != 21 && type != 29);
+  const int cap = wide ? 16 : 4;
+  return w < 1 ? 1 : w > 16 ? 4 : w > cap ? cap : w;
 }
 
 static float h2f(const uint8_t* p) { return q27o_h2f((uint16_t)(p[0] | (p[1] << 8))); }
@@ -256,10 +258,12 @@ static float chunk_t(int type, const uint8_t* blk, int s, const int8_t* u, float
 int q27o_qgemv(int type, const uint8_t* raw, int N, int K, const int8_t* xq, const float* xd, float* y, int ncols) {
   const int bb = q27o_qgemv_block_bytes(type);
   if (!bb || N % 8 || K % 256 || ncols < 1 || ncols > 4) return -1;
-  const int nb = K / 256, W = q27o_qgemv_waves(N, K);
+  const int nb = K / 256;
   for (int n = 0; n < N; n++) {
     const uint8_t* row = raw + (size_t)n * nb * bb;
     for (int c = 0; c < ncols; c++) {
+      /* three columns run as a launch of two columns and one of one */
+      const int W = q27o_qgemv_waves(type, K, ncols == 3 ? (c < 2 ? 2 : 1) : ncols);
       const int8_t* xr = xq + (size_t)c * K;
       const float* dr = xd + (size_t)c * (K / 32);
       float total = 0.0f;

@@ -6,7 +6,7 @@
 // by row inside the tile; the super-block scales go to an array ordered by (tile, block), then row. The repack only
 // moves bytes, so every weight decodes to the value it has in the GGUF block.
 //
-// Kernel (gfx950): one workgroup of W waves per tile (W = 1..4, a function of K only); lane l = 8 lb + s of wave w takes sub-block s of the blocks b = 8 w + lb, + 8 W, ... and keeps the 8 rows x
+// Kernel (gfx950): one workgroup of W waves per tile (W = 1..16, a function of K only); lane l = 8 lb + s of wave w takes sub-block s of the blocks b = 8 w + lb, + 8 W, ... and keeps the 8 rows x
 // ncols partial sums in registers, so one load of its 32 activations per column serves 8 rows. Integer dot products
 // per sub-block use v_dot4_i32_i8 (exact); the float contribution of each sub-block is the reference's expression of
 // that type (src/qgemv.cu:369-560). The 64 lane sums are added as an xor butterfly in which each exchange level sends
@@ -667,12 +667,18 @@ __device__ __forceinline__ void reduce_level(float (&a)[V], int lane) {
     a[0] += xchg<O>(a[0]);
   }
 }
-// Waves per tile: enough for every lane to take at most one block of each tile (ceil(K / 2048)), at most 4 (the
-// workgroup is these W waves). A function of K only; part of the summation order.
-constexpr int kMaxW = 4;
-constexpr int waves_per_tile(int K) {
+// Waves per tile, a function of the type, K and the column count only (part of the summation order). One column, and
+// two for all types but IQ3_XXS / IQ3_S / IQ1_M: one block of each tile per lane, ceil(K / 2048) waves, up to K = 32768
+// (16 waves); each wave adds a butterfly, which is cheap for few columns. Otherwise, and for K > 32768: at most 4 waves,
+// lanes taking several blocks. Measured (us, 5120 x 17408, 4 -> 9 waves): T = 1 Q4_K 13.1 -> 10.9, IQ3_S 18.0 -> 12.5,
+// IQ2_XXS 14.7 -> 9.7; T = 2 Q4_K 14.7 -> 13.5, IQ2_S 19.3 -> 14.7, but IQ3_S 15.8 -> 20.1, IQ1_M 18.1 -> 21.5; T = 4
+// Q4_K 18.7 -> 25.4.
+constexpr int kMaxW = 16;
+constexpr int waves_per_tile(int type, int K, int ncols) {
   const int w = (K / 256 + 7) / 8;
-  return w < 1 ? 1 : w > kMaxW ? kMaxW : w;
+  const bool wide = ncols == 1 || (ncols == 2 && type != kIQ3XXS && type != kIQ3S && type != kIQ1M);
+  const int cap = wide ? kMaxW : 4;
+  return w < 1 ? 1 : w > kMaxW ? 4 : w > cap ? cap : w;
 }
 
 template <int TYPE, int NC, bool NTP, bool ONE>
@@ -797,7 +803,7 @@ __device__ __forceinline__ void qgemv_body(Mat m, const int8_t* __restrict__ xq,
 #define Q27H_QG_WPE_ONE 4
 #endif
 template <int TYPE, int NC, bool NTP>
-__global__ void __launch_bounds__(64 * kMaxW) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+__global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                     float* __restrict__ y, int K, int W) {
   qgemv_body<TYPE, NC, NTP, false>(m, xq, xd, y, K, W);
 }
@@ -814,9 +820,10 @@ int check_type(int type) {
 
 template <int TYPE, int NC>
 void launch_gemv(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, hipStream_t s) {
-  const int W = waves_per_tile(K);
+  const int W = waves_per_tile(TYPE, K, NC);
   const int grid = m.ntiles;
-  const bool one = m.nb <= 8 * W && !((TYPE == kQ2K || TYPE == kQ4K) && NC == 4);
+  // the prefetching kernel takes at most 4 waves (lanes with several blocks); W > 4 means one block per lane
+  const bool one = m.nb <= 8 * W && (W > 4 || !((TYPE == kQ2K || TYPE == kQ4K) && NC == 4));
   if (one)
     hipLaunchKernelGGL((qgemv_one_kernel<TYPE, NC>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
   else if (K <= kNtPiecesMaxK)
@@ -843,9 +850,8 @@ extern "C" size_t q27h_qmat_bytes(int type, int N, int K) {
   return layout(type, N, K, off);
 }
 
-extern "C" int q27h_qgemv_waves(int N, int K) {
-  (void)N;
-  return waves_per_tile(K);
+extern "C" int q27h_qgemv_waves(int type, int K, int ncols) {
+  return waves_per_tile(type, K, ncols);
 }
 
 extern "C" int q27h_qmat_repack(int type, int N, int K, const void* raw, void* buf, q27h_stream_t s) {

@@ -223,5 +223,5 @@ def qgemv(m, xq, xd, y, ncols, s=None):
     check(lib().q27h_qgemv(m.type, m.N, m.K, _ptr(m.buf), _ptr(xq), _ptr(xd), _ptr(y), ncols, _stream(s)))
 
 
-def qgemv_waves(N, K):
-    return int(lib().q27h_qgemv_waves(N, K))
+def qgemv_waves(type_, K, ncols):
+    return int(lib().q27h_qgemv_waves(type_, K, ncols))

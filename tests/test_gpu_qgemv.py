@@ -56,6 +56,21 @@ def test_qgemv_columns(q27, oracle, dev, type_, ncols):
     assert_bits_equal(got, want, f"qgemv type {type_} ncols {ncols}")
 
 
+@pytest.mark.parametrize("type_", TYPES)
+@pytest.mark.parametrize("ncols", [1, 2, 3])
+def test_qgemv_columns_wide_k(q27, oracle, dev, type_, ncols):
+    """One or two columns over long rows: up to 16 waves per tile (K = 17408: 9 waves, 68 blocks in 72 slots;
+    K = 32768: 16 waves)."""
+    for N, K in [(512, 17408), (64, 32768)]:
+        say(f"qgemv type {type_} {N}x{K} ncols={ncols}")
+        r = cd.rng(450 + type_ + ncols + K)
+        raw = cd.random_weights(r, type_, N, K)
+        xq, xd = cd.q8_activations(oracle, r, ncols, K)
+        got = _run(q27, dev, type_, N, K, raw, xq, xd, ncols)
+        want = oracle.qgemv(type_, raw, N, K, xq, xd, ncols)
+        assert_bits_equal(got, want, f"qgemv type {type_} {N}x{K} ncols {ncols}")
+
+
 def test_qgemv_small_and_edge_shapes(q27, oracle, dev):
     """One tile, one block per row, and partial 8-block groups; zero activations and wide scale ranges."""
     for type_ in TYPES:

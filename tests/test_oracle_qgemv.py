@@ -237,10 +237,17 @@ def test_qgemv_matches_float64_dequant(oracle, type_, shape):
 
 def test_qgemv_waves_rule_matches_library(oracle, q27):
     lib = q27.lib()
-    for N in [8, 1024, 5120, 248320]:
-        for K in [256, 1024, 2048, 2304, 4096, 5120, 6144, 8192, 10240, 17408, 32768, 40960]:
-            assert lib.q27h_qgemv_waves(N, K) == oracle.qgemv_waves(N, K), (N, K)
-    assert [oracle.qgemv_waves(8, K) for K in (256, 2048, 2304, 5120, 8192, 17408, 40960)] == [1, 1, 2, 3, 4, 4, 4]
+    for type_ in cd.QG_BLOCK:
+        for nc in (1, 2, 3, 4):
+            for K in [256, 1024, 2048, 2304, 4096, 5120, 6144, 8192, 10240, 17408, 32768, 33024, 40960]:
+                assert lib.q27h_qgemv_waves(type_, K, nc) == oracle.qgemv_waves(type_, K, nc), (type_, K, nc)
+    Ks = (256, 2048, 2304, 5120, 8192, 17408, 32768, 33024, 40960)
+    wide, narrow = [1, 1, 2, 3, 4, 9, 16, 4, 4], [1, 1, 2, 3, 4, 4, 4, 4, 4]
+    assert [oracle.qgemv_waves(cd.Q4_K, K, 1) for K in Ks] == wide
+    assert [oracle.qgemv_waves(cd.IQ3_S, K, 1) for K in Ks] == wide
+    assert [oracle.qgemv_waves(cd.Q4_K, K, 2) for K in Ks] == wide
+    assert [oracle.qgemv_waves(cd.IQ3_S, K, 2) for K in Ks] == narrow
+    assert [oracle.qgemv_waves(cd.Q4_K, K, 4) for K in Ks] == narrow
 
 
 def test_qgemv_rejects_bad_shapes(oracle):
