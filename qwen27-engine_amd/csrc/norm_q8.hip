@@ -34,7 +34,7 @@ enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2, kAddQ8Wire = 3 };
 #define Q27H_NT_GATED 0
 #endif
 #ifndef Q27H_GATED_G
-#define Q27H_GATED_G 2  // 25.2 us in the pass vs 25.5 with 1 and 27.7 with 4
+#define Q27H_GATED_G 1  // the prefill pass (2048 tokens, 48 launches): 9.824 ms against 9.892 ms with 2 (three A/B runs on one box)
 #endif
 constexpr int kGatedG = Q27H_GATED_G;
 constexpr int kLatencyRows = 64;  // row launches up to this many rows take the latency-bound kernel variants  // groups of 8 heads per workgroup in gated_rmsnorm_q8
@@ -164,8 +164,10 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
 // A 256-thread workgroup covers U * 1024 consecutive values; in each 1024-value chunk thread t handles the 4
 // values at 32 (t / 8) + 4 quad_of_lane(t % 8) (n % 32 == 0, so a q8 block is the 8 lanes of one group). All loads of a thread are
 // issued before any arithmetic so U * 16 (quantize) or U * 32 (swiglu) bytes per lane are in flight.
+// Chunks per workgroup, measured in the prefill pass (2048 tokens; two A/B runs on one box): swiglu 1 (9.972 ms
+// against 10.010 ms with 2), quantize 2 (10.040 ms with 1).
 #ifndef Q27H_FLAT_U
-#define Q27H_FLAT_U 2
+#define Q27H_FLAT_U 1
 #endif
 #ifndef Q27H_QUANT_U
 #define Q27H_QUANT_U 2
