@@ -31,9 +31,9 @@ N_LAYER, N_CTX, VOCAB = 64, 180224, 248320
 EPS = 1e-6
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per swiglu_q8 launch at M = 2048, measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over the prefill
-# pass and scaled by the copy-kernel calibration (FETCH x 2.000, WRITE x 1.000): 139301 KiB and 47872 KiB
+# pass and scaled by the copy-kernel calibration (FETCH x 2.000, WRITE x 1.000): 139291 KiB and 47872 KiB
 # (profiles/hbm_traffic_prefill_pass.md). The counters cannot be read from inside this process.
-SWIGLU_TRAFFIC_BYTES = int((139301 * 2.0 + 47872 * 1.0) * 1024)
+SWIGLU_TRAFFIC_BYTES = int((139291 * 2.0 + 47872 * 1.0) * 1024)
 
 
 def is_attn(il):
