@@ -366,14 +366,13 @@ int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* 
                 int8_t* xq, float* xd, float* xs, int rows, q27h_stream_t s, const uint8_t* wown = nullptr,
                 const uint8_t* wrecv = nullptr, int qb_shift = 0) {
   if (rows == 0) return Q27H_OK;
-  // up to kLatencyRows rows a launch is latency-bound (one workgroup per row, a few per chip): branch-free quotients
-  // (a 1024-thread form with 5 values per lane, the reference's layout, measured slower: 4.0 against 3.3 us per node)
-  if (rows <= kLatencyRows)
-    hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
-                       xq, xd, xs, wown, wrecv, qb_shift);
-  else
-    hipLaunchKernelGGL((row_norm_q8_kernel<MODE, false>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps,
-                       h, xq, xd, xs, wown, wrecv, qb_shift);
+  // Branch-free quotients (q8_quot_exact) at every size: latency-bound launches (a few workgroups per chip) gain the
+  // shorter chain, and in the 2048-row prefill pass they measured 9.72 against 9.86 ms per pass with the reciprocal
+  // fast path (two A/B runs on one box; the row kernel's waves otherwise often wait on a fallback block). A
+  // 1024-thread form with 5 values per lane, the reference's layout, measured slower: 4.0 against 3.3 us per decode
+  // node.
+  hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
+                     xq, xd, xs, wown, wrecv, qb_shift);
   return check_launch(fn);
 }
 
