@@ -316,9 +316,11 @@ __device__ __forceinline__ bool q8_quot_exact(const float (&y)[N], float d, int 
 }
 
 // roundf(y / d) for |y| <= 127 d (the q8_1 rule of src/common.cuh:76; q = 0 when d == 0), four values at a time.
-// For 2^-126 <= d <= 2^126, a = y * rcp(d) (v_rcp_f32, 1 ulp) is within 127 * 2^-22 < 3.1e-5 of the exact quotient,
-// so unless a lies within 2^-12 of a half-integer it rounds to the same integer as the correctly rounded quotient,
-// and rintf == roundf there. Values near a half-integer, NaN, d == 0 and d outside that range take the IEEE quotient:
+// For 2^-126 <= d <= 2^126, a = y * rcp(d) (v_rcp_f32 within 1 ulp, then one rounding) is within
+// 127 (2^-23 + 2^-24) < 2.3e-5 of the exact quotient y / d, and the correctly rounded quotient within 2^-18 (half an ulp
+// below 128) of it; so unless a lies within 2.7e-5 of a half-integer, a and the IEEE quotient round to the same
+// integer, and rintf == roundf there. The guard band is 2^-14 = 6.1e-5 (2^-12 measured 40 us per prefill pass slower:
+// a wave takes the branch when any of its values falls in the band). Values near a half-integer, NaN, d == 0 and d outside that range take the IEEE quotient:
 // one branch per four values, almost never taken.
 __device__ __forceinline__ void q8_round_div4(const float (&y)[4], float d, int (&q)[4]) {
   const float rd = __builtin_amdgcn_rcpf(d);
@@ -327,7 +329,7 @@ __device__ __forceinline__ void q8_round_div4(const float (&y)[4], float d, int 
   for (int c = 0; c < 4; c++) {
     const float a = y[c] * rd;
     const float r = __builtin_rintf(a);
-    slow |= !(__builtin_fabsf(a - r) < 0.5f - 0x1p-12f);
+    slow |= !(__builtin_fabsf(a - r) < 0.5f - 0x1p-14f);
     q[c] = (int)r;
   }
   if (slow) {

@@ -156,6 +156,29 @@ def test_q8_rounding_near_half_integers(q27, oracle, T, reps):
         assert_bits_equal(T.down(got), want, what)
 
 
+@pytest.mark.parametrize("reps", [1, 3])
+def test_q8_rounding_beside_the_guard_band(q27, oracle, T, reps):
+    """Quotients 4 to 64 ulps from k + 0.5 (2^-15 .. 2^-11 for |q| in [64, 128)): on both sides of the reciprocal
+    path's guard band around half-integers, so values that the fast path rounds by itself are checked next to those it
+    hands to the IEEE quotient."""
+    say(f"q8_1 rounding beside the guard band reps={reps}")
+    r = cd.rng(124)
+    nblk = 4096
+    amax = np.exp(r.uniform(-8, 8, nblk)).astype(np.float32)
+    d = amax / np.float32(127)
+    k = r.integers(-126, 126, (nblk, 31)).astype(np.float32)
+    y = ((k + np.float32(0.5)) * d[:, None]).astype(np.float32)
+    ulps = r.integers(4, 65, (nblk, 31)).astype(np.int32) * np.where(r.random((nblk, 31)) < 0.5, -1, 1).astype(np.int32)
+    y = (y.view(np.int32) + ulps).view(np.float32)
+    x = np.tile(np.concatenate([amax[:, None], y], 1).reshape(-1), reps)
+    assert (x.size <= LAT_LIMIT) == (reps == 1)
+    xq, xd, xs = q8_bufs(T, x.size, True)
+    q27.ops.quantize_q8_1(T.up(x), xq, xd, x.size, 1, None, xs)
+    oq, od, os_ = oracle.quantize_q8_1(x, x.size, 1, with_xs=True)
+    for got, want, what in ((xq, oq, "xq"), (xd, od, "xd"), (xs, os_, "xs")):
+        assert_bits_equal(T.down(got), want, what)
+
+
 @pytest.mark.parametrize("reps", [1, 6])
 def test_q8_tiny_and_huge_scales(q27, oracle, T, reps):
     """Blocks whose scale d = amax / 127 is subnormal or tiny (the reciprocal path hands them to the IEEE quotient) or
