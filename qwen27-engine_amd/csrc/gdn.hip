@@ -12,7 +12,7 @@
 #include "q27h_internal.h"
 
 #ifndef Q27H_GDN_CH
-#define Q27H_GDN_CH 4
+#define Q27H_GDN_CH 2
 #endif
 #ifndef Q27H_GDN_FAST_SILU
 #define Q27H_GDN_FAST_SILU 1
@@ -67,10 +67,10 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
 
 // Prefill: 32 lanes per (head of 128 channels, span of SPAN tokens), a workgroup = 8 neighbouring heads of one
 // span. The lanes walk the span in batches of CH tokens, the rows of the next batch loaded before the current one is
-// computed. The conv window of a span starts with the 3 rows before it. With SPAN == CH (the default, 4) a span
-// loads all its rows first, so its last 3 rows are read at the same moment as the next span (the next tile of the
-// same XCD in the XCD-major order) reads them as its window: L2 hits, and the kernel's HBM reads stay within 4% of
-// the single pass over the input. Longer spans cut that re-read but leave fewer, longer workgroups (measured: 4 tokens
+// computed. The conv window of a span starts with the 3 rows before it. Spans of 4 tokens in batches of 2 (the
+// second batch requested before the first is computed; 30 us less per 2048-token prefill pass than one batch of 4,
+// A/B runs of the pass): a span's last rows are read at about the moment the next span (the next tile of the same XCD
+// in the XCD-major order) reads them as its window, so they are L2 hits. Longer spans cut that re-read but leave fewer, longer workgroups (measured: 4 tokens
 // 31.7 us, 8 tokens 32.7 us, 16 tokens 34.5 us at M = 2048).
 template <int CH, int SPAN>
 __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __restrict__ x, const float* __restrict__ cw,
