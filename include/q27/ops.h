@@ -2,8 +2,9 @@
 // (namespace q27, same names, parameter order and defaults; cudaStream_t becomes hipStream_t). Each function
 // forwards to the C ABI of include/q27h.h and throws std::runtime_error on a non-zero status, as the reference
 // launchers throw on bad shapes (src/ops.cu:699,704,724,734) and through CK (src/common.cuh:11-12).
-// Only the functions of the fused-op path are declared; the GEMV, attention and delta-rule kernels of src/ops.h
-// are outside this library.
+// Declared here: the fused per-layer ops and their unfused twins, the delta-rule recurrence gdn_step and the bf16
+// pair GEMV gemv_bf16_pair of src/ops.h. The quantized GEMV is in qmat.h, the prefill row ops in prefill.h; the
+// attention kernels of src/ops.h (attn_decode, attn_prefill) are outside this library.
 #pragma once
 #include <hip/hip_bf16.h>
 #include <hip/hip_runtime_api.h>

@@ -143,3 +143,29 @@ def gdn_inputs(r, T, H=HV, HK=KH, planes_std=0.5):
     beta = (1.0 / (1.0 + np.exp(-r.standard_normal(T * H)))).astype(np.float32)
     planes = normal(r, 4 * H * 128 * 128, std=planes_std)
     return x.reshape(-1).copy(), stride, g, beta, planes
+
+
+def round_half_away(r32):
+    """roundf of float32 values, computed in float64 (exact for float32 inputs)."""
+    r = r32.astype(np.float64)
+    return np.sign(r) * np.floor(np.abs(r) + 0.5)
+
+
+def near_tie_blocks(seed, nblk, log2_amax=(-20, 20), k_min=0, signed=True):
+    """Blocks of 32 whose values sit within a few ulps of (k + 1/2) * d, where d = amax / 127 in float32.
+
+    Value 0 of each block is the amax (so it fixes d); the others are k + 1/2 steps of d nudged by -3..3 ulps, which
+    is where the quotient and the product with the rounded reciprocal can round differently."""
+    r = np.random.default_rng(seed)
+    amax = np.exp2(r.integers(*log2_amax, nblk)).astype(np.float32) * r.uniform(1, 2, nblk).astype(np.float32)
+    d = amax / np.float32(127)
+    k = r.integers(k_min, 126, (nblk, 31)).astype(np.float32)
+    base = ((k + np.float32(0.5)) * d[:, None]).astype(np.float32)
+    ulp = r.integers(-3, 4, (nblk, 31)).astype(np.int32)
+    y = (base.view(np.int32) + ulp).view(np.float32)
+    flip = (lambda shape: np.where(r.random(shape) < 0.5, -1, 1)) if signed else (lambda shape: np.ones(shape))
+    sign = flip((nblk, 31)).astype(np.float32)
+    blk = np.empty((nblk, 32), np.float32)
+    blk[:, 0] = amax * flip(nblk).astype(np.float32)
+    blk[:, 1:] = np.minimum(np.abs(y), amax[:, None]) * sign
+    return blk
