@@ -24,19 +24,22 @@ struct RopeFreqs {
 };
 
 
-// One wave per (token, group of HPW heads): HPW = 2 for batches (the 28 heads of a token are 14 waves, wave w taking
-// heads w and w + 14, so the 4 K heads with their q8/f16 cache work are spread over 4 waves instead of making one
-// wave the straggler; measured 26.5 us against 28.9 us with 4 heads per wave at 2048 tokens), HPW = 1 for a few
-// tokens, where the shorter chain per wave matters more than loads in flight. The 32 rotary angles of the token are
-// evaluated
-// once per wave (lane j < 32 takes pair j) and handed to the lanes that need them with ds_bpermute; the head
-// vectors of the whole group are loaded before any arithmetic.
+// One wave per (token, group of HPW heads). Batches: HPW = 4, one workgroup of 7 waves per token (TOKWG below), wave w
+// taking heads w, w + 7, w + 14, w + 21, so the 4 K heads with their q8/f16 cache work sit in 4 different waves
+// (2048 tokens: 23.9 us against 26.3 us for 2 heads per wave, both one workgroup per token, and 26.2 us for 2 heads per
+// wave with every wave evaluating the angles). A few tokens: HPW = 1 and four independent waves per workgroup,
+// where the shorter chain per wave matters more than loads in flight; every wave then evaluates the 32 angles of
+// its token (lane j < 32 takes pair j) and hands them to the lanes that need them with ds_bpermute. The head vectors
+// of the whole group are loaded before any arithmetic.
 #ifndef Q27H_ATTN_HPW
-#define Q27H_ATTN_HPW 2
+#define Q27H_ATTN_HPW 4
 #endif
 
-template <int HPW>
-__global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict__ qg, const float* __restrict__ k,
+// TOKWG: one workgroup per token (its waves = the token's head groups). Wave 0 evaluates the 32 angles once for the
+// token and hands them out through LDS, instead of every wave of the token evaluating them: the rotary setup (the
+// frequency select and the double-precision sin / cos) was about a third of each wave's VALU instructions.
+template <int HPW, bool TOKWG>
+__global__ void __launch_bounds__(1024) attn_prep_kernel(const float* __restrict__ qg, const float* __restrict__ k,
                                                         const float* __restrict__ v, const float* __restrict__ q_norm,
                                                         const float* __restrict__ k_norm, float* __restrict__ qn,
                                                         void* __restrict__ kcache, void* __restrict__ vcache,
@@ -45,10 +48,16 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
                                                         const int* __restrict__ rdelta) {
   const int nh = nqh + nkvh;
   const int wpt = (nh + HPW - 1) / HPW;  // waves per token
-  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar registers
-  if (wave >= T * wpt) return;  // whole waves leave together
-  const int tok = wave / wpt;
-  const int hw = wave % wpt;  // heads hw, hw + wpt, hw + 2 wpt, ...: the K heads (the last ones) fall in different waves
+  int tok, hw;  // heads hw, hw + wpt, hw + 2 wpt, ...: the K heads (the last ones) fall in different waves
+  if constexpr (TOKWG) {
+    tok = blockIdx.x;  // blockDim.x = 64 wpt: every wave of the workgroup has a head group
+    hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  } else {
+    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar registers
+    if (wave >= T * wpt) return;  // whole waves leave together
+    tok = wave / wpt;
+    hw = wave % wpt;
+  }
   const int nhw = (nh - hw + wpt - 1) / wpt;
   const int p = threadIdx.x & 63;
   const int off = 32 * (p >> 3) + block_offset(p);  // this lane's 4 head dims (32-value block layout)
@@ -71,29 +80,48 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(const float* __restrict_
   // ---- rotary angles of the token, lane j < 32 evaluating pair j, from scalar loads and kernel arguments only
   // (no wait on the vector loads above, so the sin/cos run while the head vectors are in flight)
   const int j32 = p & 31;
-  int rp;
-  if (rope3) {
-    const int r0 = rope3[tok * 3], r1 = rope3[tok * 3 + 1], r2 = rope3[tok * 3 + 2];
-    const int m = j32 % 3;
-    rp = m == 0 ? r0 : m == 1 ? r1 : r2;
-  } else {
-    rp = pos - (rdelta ? *rdelta : 0);
-  }
-  float fj = fr.f[0];  // fr.f[j32], selected from the argument registers
+  auto angle = [&](float& sn_j, float& cs_j) {
+    int rp;
+    if (rope3) {
+      const int r0 = rope3[tok * 3], r1 = rope3[tok * 3 + 1], r2 = rope3[tok * 3 + 2];
+      const int m = j32 % 3;
+      rp = m == 0 ? r0 : m == 1 ? r1 : r2;
+    } else {
+      rp = pos - (rdelta ? *rdelta : 0);
+    }
+    float fj = fr.f[0];  // fr.f[j32], selected from the argument registers
 #pragma unroll
-  for (int m = 1; m < 32; m++) {
-    float fm = fr.f[m];
-    asm("" : "+s"(fm));  // keeps the selects (no indexed load from the argument segment, which would wait behind the head loads)
-    fj = j32 == m ? fm : fj;
-  }
-  float sn_j, cs_j;
-  q27_sincos((float)rp * fj, &sn_j, &cs_j);
+    for (int m = 1; m < 32; m++) {
+      float fm = fr.f[m];
+      asm("" : "+s"(fm));  // keeps the selects (no indexed load from the argument segment, which would wait behind the head loads)
+      fj = j32 == m ? fm : fj;
+    }
+    q27_sincos((float)rp * fj, &sn_j, &cs_j);
+  };
   float snc[4], csc[4];
+  if constexpr (TOKWG) {
+    __shared__ float s_sc[2][32];
+    if (hw == 0 && p < 32) {
+      float sn_j, cs_j;
+      angle(sn_j, cs_j);
+      s_sc[0][p] = sn_j;
+      s_sc[1][p] = cs_j;
+    }
+    __syncthreads();
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const int j = (off + c) & 31;
-    snc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, sn_j)));
-    csc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, cs_j)));
+    for (int c = 0; c < 4; c++) {
+      snc[c] = s_sc[0][(off + c) & 31];
+      csc[c] = s_sc[1][(off + c) & 31];
+    }
+  } else {
+    float sn_j, cs_j;
+    angle(sn_j, cs_j);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int j = (off + c) & 31;
+      snc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, sn_j)));
+      csc[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(j << 2, __builtin_bit_cast(int, cs_j)));
+    }
   }
   const bool valid = pos >= 0 && pos < n_ctx;  // uniform over the wave
   const size_t so = (size_t)nkvh * n_ctx * 256;
@@ -206,13 +234,17 @@ extern "C" int q27h_attn_prep(const float* qg, const float* k, const float* v, c
   const int nh = nqh + nkvh;
   if ((long)T * nh < 2048) {
     const long waves = (long)T * nh;
-    hipLaunchKernelGGL(attn_prep_kernel<1>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm,
-                       k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
+    hipLaunchKernelGGL((attn_prep_kernel<1, false>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k,
+                       v, q_norm, k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
   } else {
     constexpr int hpw = Q27H_ATTN_HPW;
-    const long waves = (long)T * ((nh + hpw - 1) / hpw);
-    hipLaunchKernelGGL(attn_prep_kernel<hpw>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream_of(s), qg, k, v, q_norm,
-                       k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
+    const int wpt = (nh + hpw - 1) / hpw;
+    if (wpt <= 16)
+      hipLaunchKernelGGL((attn_prep_kernel<hpw, true>), dim3((unsigned)T), dim3(64 * wpt), 0, stream_of(s), qg, k, v, q_norm,
+                         k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
+    else
+      hipLaunchKernelGGL((attn_prep_kernel<hpw, false>), dim3((unsigned)(((long)T * wpt + 3) / 4)), dim3(256), 0, stream_of(s),
+                         qg, k, v, q_norm, k_norm, qn, kcache, vcache, pos0, T, eps, fr, nqh, nkvh, n_ctx, q8, rope3, rdelta);
   }
   return check_launch("attn_prep");
 }

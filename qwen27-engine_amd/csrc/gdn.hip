@@ -11,14 +11,8 @@
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
-#ifndef Q27H_GDN_CH
-#define Q27H_GDN_CH 2
-#endif
-#ifndef Q27H_GDN_FAST_SILU
-#define Q27H_GDN_FAST_SILU 1
-#endif
 #ifndef Q27H_GDN_SPAN
-#define Q27H_GDN_SPAN 4
+#define Q27H_GDN_SPAN 8
 #endif
 
 namespace q27h {
@@ -65,54 +59,48 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
   g[i] = q27_softplus(a[i] + dt_bias[hv]) * ssm_a[hv];
 }
 
-// Prefill: 32 lanes per (head of 128 channels, span of SPAN tokens), a workgroup = 8 neighbouring heads of one
-// span. The lanes walk the span in batches of CH tokens, the rows of the next batch loaded before the current one is
-// computed. The conv window of a span starts with the 3 rows before it. Spans of 4 tokens in batches of 2 (the
-// second batch requested before the first is computed; 30 us less per 2048-token prefill pass than one batch of 4,
-// A/B runs of the pass): a span's last rows are read at about the moment the next span (the next tile of the same XCD
-// in the XCD-major order) reads them as its window, so they are L2 hits. Longer spans cut that re-read but leave fewer, longer workgroups (measured: 4 tokens
-// 31.7 us, 8 tokens 32.7 us, 16 tokens 34.5 us at M = 2048).
-template <int CH, int SPAN>
+// Prefill: 32 lanes per (head of 128 channels, span of SPAN tokens), a workgroup = 8 neighbouring heads of one span.
+// Tiles run in span-major order (the head groups of a span are neighbouring workgroups), so the workgroups in flight
+// read and write whole 40 KB rows of the [M][C] arrays: reading 4 KB column pieces of many rows instead, as a
+// group-major order does, costs 13% of the bandwidth (measured with a copy of the same shape). Every row of the span
+// and the 3-row window before it are loaded up front, then the tokens are computed in order with the window kept in
+// registers. The gates (sigmoid / softplus of the H value heads of every token) are not evaluated by the conv lanes:
+// the first `gate_blocks` workgroups of the grid take one (token, value head) per lane.
+template <int SPAN>
 __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __restrict__ x, const float* __restrict__ cw,
                                                                float* __restrict__ planes, const int* __restrict__ in_plane,
                                                                float* __restrict__ y, int C, int T, int n_norm_heads,
                                                                float eps, const float* __restrict__ a,
                                                                const float* __restrict__ b, const float* __restrict__ ssm_a,
                                                                const float* __restrict__ dt_bias, float* __restrict__ g,
-                                                               float* __restrict__ beta, int H, int nspans, int tiles_per_xcd) {
-  static_assert(SPAN % CH == 0 && SPAN >= 3, "a span is whole batches and covers the 3-input window");
+                                                               float* __restrict__ beta, int H, int nspans, int gate_blocks) {
+  static_assert(SPAN >= 3, "a span covers the 3-input window");
+  if ((int)blockIdx.x < gate_blocks) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < T * H) gate_one(a, b, ssm_a, dt_bias, g, beta, i / H, H, i % H);
+    return;
+  }
   const int nheads = C / 128;
   const int ngroups = (nheads + 7) / 8;
-  const int tile = (blockIdx.x & 7) * tiles_per_xcd + (blockIdx.x >> 3);  // XCD-major order of the tiles
-  if (tile >= ngroups * nspans) return;
-  const int group = tile / nspans, sp = tile % nspans;
+  const int tile = blockIdx.x - gate_blocks;
+  const int group = tile % ngroups, sp = tile / ngroups;
   const int head = group * 8 + (threadIdx.x >> 5);
   if (head >= nheads) return;  // whole halves leave together
   const int p = threadIdx.x & 31;
   const int cb = head * 128 + l2_lane(p);  // channels cb + 32k
   const int t0 = sp * SPAN, t1 = min(T, t0 + SPAN);
-  const int pin = *in_plane;
-  auto load_batch = [&](int tb, float (&dst)[CH][4]) {
+  float xr[SPAN][4];
 #pragma unroll
-    for (int i = 0; i < CH; i++) {
-      if (tb + i < t1) {
-        const float* xr = x + (size_t)(tb + i) * C + cb;
+  for (int i = 0; i < SPAN; i++) {
+    if (t0 + i < t1) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) dst[i][k] = xr[32 * k];
-      }
+      for (int k = 0; k < 4; k++) xr[i][k] = x[(size_t)(t0 + i) * C + cb + 32 * k];
     }
-  };
-  float xb[CH][4];
-  load_batch(t0, xb);
-  float w[4][4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const float4 wv = ld4(cw + 4 * (size_t)(cb + 32 * k));
-    w[k][0] = wv.x; w[k][1] = wv.y; w[k][2] = wv.z; w[k][3] = wv.w;
   }
   // conv window: s0, s1, s2 = inputs t0-3, t0-2, t0-1 (state plane `pin` before the batch)
   float s0[4], s1[4], s2[4];
   if (t0 == 0) {
+    const int pin = *in_plane;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const float* st = planes + ((size_t)pin * C + cb + 32 * k) * 3;
@@ -126,44 +114,32 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
       s2[k] = x[(size_t)(t0 - 1) * C + cb + 32 * k];
     }
   }
+  float w[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const float4 wv = ld4(cw + 4 * (size_t)(cb + 32 * k));
+    w[k][0] = wv.x; w[k][1] = wv.y; w[k][2] = wv.z; w[k][3] = wv.w;
+  }
+  loads_issued();
   const bool norm = head < n_norm_heads;
 #pragma unroll
-  for (int j = 0; j < SPAN / CH; j++) {
-    const int tb = t0 + j * CH;
-    if (tb >= t1) break;
-    float xn[CH][4];
-    if (j + 1 < SPAN / CH && tb + CH < t1) load_batch(tb + CH, xn);
+  for (int i = 0; i < SPAN; i++) {
+    const int t = t0 + i;
+    if (t >= t1) break;
+    float cv[4], cur[4];
 #pragma unroll
-    for (int i = 0; i < CH; i++) {
-      const int t = tb + i;
-      if (t >= t1) break;
-      float cv[4], cur[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        cv[k] = conv4(s0[k], s1[k], s2[k], xb[i][k], w[k]);
-        s0[k] = s1[k]; s1[k] = s2[k]; s2[k] = xb[i][k];
-      }
-#if Q27H_GDN_FAST_SILU
-      q27_silu_n(cv, cur);
-#else
-#pragma unroll
-      for (int k = 0; k < 4; k++) cur[k] = q27_silu(cv[k]);
-#endif
-      if (norm) l2_head_lanes(cur, eps);
-      float* yr = y + (size_t)t * C + cb;
-#pragma unroll
-      for (int k = 0; k < 4; k++) st_f32<kGdnNT>(yr + 32 * k, cur[k]);
+    for (int k = 0; k < 4; k++) {
+      cv[k] = conv4(s0[k], s1[k], s2[k], xr[i][k], w[k]);
+      s0[k] = s1[k]; s1[k] = s2[k]; s2[k] = xr[i][k];
     }
+    q27_silu_n(cv, cur);
+    if (norm) l2_head_lanes(cur, eps);
+    float* yr = y + (size_t)t * C + cb;
 #pragma unroll
-    for (int i = 0; i < CH; i++)
-#pragma unroll
-      for (int k = 0; k < 4; k++) xb[i][k] = xn[i][k];
-  }
-  if (!norm) {
-    const int hv = head - n_norm_heads;
-    for (int t = t0 + p; t < t1; t += 32) gate_one(a, b, ssm_a, dt_bias, g, beta, t, H, hv);
+    for (int k = 0; k < 4; k++) st_f32<kGdnNT>(yr + 32 * k, cur[k]);
   }
   if (t1 == T) {  // state after the batch: inputs T-3 .. T-1 (from the old state when T < 3)
+    const int pin = *in_plane;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       float* o = planes + ((size_t)(pin == 0 ? 1 : 0) * C + cb + 32 * k) * 3;
@@ -352,10 +328,9 @@ extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* plan
   constexpr int span = Q27H_GDN_SPAN;  // tokens per half-wave
   const int nspans = (M + span - 1) / span;
   const long tiles = (long)((C / 128 + 7) / 8) * nspans;
-  const int tiles_per_xcd = (int)((tiles + 7) / 8);
-  hipLaunchKernelGGL((gdn_conv_prefill_kernel<Q27H_GDN_CH, span>), dim3((unsigned)(8 * tiles_per_xcd)), dim3(256), 0,
-                     stream_of(s), x, w, planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H,
-                     nspans, tiles_per_xcd);
+  const int gate_blocks = (int)(((long)M * H + 255) / 256);
+  hipLaunchKernelGGL((gdn_conv_prefill_kernel<span>), dim3((unsigned)(tiles + gate_blocks)), dim3(256), 0, stream_of(s), x, w,
+                     planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, nspans, gate_blocks);
   return check_launch("gdn_conv_prefill");
 }
 

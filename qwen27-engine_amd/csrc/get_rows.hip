@@ -96,7 +96,7 @@ __device__ __forceinline__ void decode4<kQ80>(const uint8_t* __restrict__ b, int
 }
 
 #ifndef Q27H_NT_ROWS
-#define Q27H_NT_ROWS 0
+#define Q27H_NT_ROWS 1
 #endif
 constexpr bool kRowsNT = Q27H_NT_ROWS;
 

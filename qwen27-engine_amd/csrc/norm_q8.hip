@@ -370,7 +370,8 @@ int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* 
   // shorter chain, and in the 2048-row prefill pass they measured 9.72 against 9.86 ms per pass with the reciprocal
   // fast path (two A/B runs on one box; the row kernel's waves otherwise often wait on a fallback block). A
   // 1024-thread form with 5 values per lane, the reference's layout, measured slower: 4.0 against 3.3 us per decode
-  // node.
+  // node. A persistent form (a grid of 1-4 workgroups per CU, each walking rows with the next row's loads in flight)
+  // measured slower at 2048 rows: 30.0-31.7 against 27.6 us for sum_norm_rows.
   hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
                      xq, xd, xs, wown, wrecv, qb_shift);
   return check_launch(fn);

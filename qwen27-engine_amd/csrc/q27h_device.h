@@ -12,6 +12,7 @@
 namespace q27h {
 
 constexpr int kRowN = 5120;  // hidden size of the row kernels (n must be 5120, src/ops.cu:699)
+constexpr int kCUs = 256;    // compute units of an MI355X (8 XCDs of 32), the grid unit of the persistent kernels
 
 // ---------------------------------------------------------------- lane exchange
 // Value of lane (lane ^ M), M in {1, 2, 4, 7, 8, 16, 24}: stays inside an aligned group of 32 lanes.
