@@ -801,6 +801,10 @@ __device__ __forceinline__ void qgemv_body(Mat m, const int8_t* __restrict__ xq,
 // Q4_K with four columns keep the prefetching kernel). The additions are the same, so the results are identical.
 // Its wide pieces are always read with nontemporal loads: ordinary loads at K = 17408 measured 2-5% slower (Q6_K T = 1
 // 13.7 -> 14.3 us), the opposite of the prefetching kernel.
+// IQ3_S with four columns needs a few more than 128 VGPRs here and spills 12 bytes per lane (about 2 MB of scratch
+// traffic per 17408 x 5120 launch); both ways of avoiding the spill measured slower (us, 17408 x 5120 / 5120 x 17408,
+// T = 4): 3 waves per SIMD for that instantiation 21.3 / 20.4 against 19.8 / 20.5, and the row's codebook reads in two
+// halves 20.5 / 23.9 against 19.7 / 20.2.
 #ifndef Q27H_QG_WPE_ONE
 #define Q27H_QG_WPE_ONE 4
 #endif
