@@ -60,9 +60,9 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
 }
 
 // Prefill: 32 lanes per (head of 128 channels, span of SPAN tokens), a workgroup = 8 neighbouring heads of one span.
-// Tiles run in span-major order (the head groups of a span are neighbouring workgroups), so the workgroups in flight
-// read and write whole 40 KB rows of the [M][C] arrays: reading 4 KB column pieces of many rows instead, as a
-// group-major order does, costs 13% of the bandwidth (measured with a copy of the same shape). Every row of the span
+// Each XCD runs its share of the tiles in span-major order (the head groups of a span are neighbouring workgroups),
+// so the workgroups in flight read and write whole 40 KB rows of the [M][C] arrays: reading 4 KB column pieces of
+// many rows instead, as a group-major order does, costs 13% of the bandwidth (measured with a copy of the same shape). Every row of the span
 // and the 3-row window before it are loaded up front, then the tokens are computed in order with the window kept in
 // registers. The gates (sigmoid / softplus of the H value heads of every token) are not evaluated by the conv lanes:
 // the first `gate_blocks` workgroups of the grid take one (token, value head) per lane. Workgroups that walk 16-64
@@ -84,7 +84,12 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
   }
   const int nheads = C / 128;
   const int ngroups = (nheads + 7) / 8;
-  const int tile = blockIdx.x - gate_blocks;
+  // workgroups are handed to the 8 XCDs round-robin, so the workgroups with one value x of bi % 8 share an XCD; they
+  // take the tiles [x tpx, (x + 1) tpx) in span-major order, and the window rows of a span were loaded by the span
+  // before it on the same XCD (L2 hits)
+  const int ntiles = ngroups * nspans, tpx = (ntiles + 7) / 8, bi = blockIdx.x - gate_blocks;
+  const int tile = (bi & 7) * tpx + (bi >> 3);
+  if (tile >= ntiles) return;
   const int group = tile % ngroups, sp = tile / ngroups;
   const int head = group * 8 + (threadIdx.x >> 5);
   if (head >= nheads) return;  // whole halves leave together
@@ -330,7 +335,7 @@ extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* plan
   constexpr int span = Q27H_GDN_SPAN;  // tokens per half-wave
   const int gate_blocks = (int)(((long)M * H + 255) / 256);
   const int nspans = (M + span - 1) / span;
-  const long tiles = (long)((C / 128 + 7) / 8) * nspans;
+  const long tiles = ((long)((C / 128 + 7) / 8) * nspans + 7) / 8 * 8;  // a whole number of tiles per XCD
   hipLaunchKernelGGL((gdn_conv_prefill_kernel<span>), dim3((unsigned)(tiles + gate_blocks)), dim3(256), 0, stream_of(s), x, w,
                      planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, nspans, gate_blocks);
   return check_launch("gdn_conv_prefill");
