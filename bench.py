@@ -819,6 +819,8 @@ def main():
                     help="only run eight decode GEMV launches of this shape over four uploaded copies of a random "
                          "matrix (the workload of the rocprofv3 counter runs of the GEMV), then exit")
     ap.add_argument("--calib-copy", action="store_true", help="also run a plain 256 MiB copy (rocprof counter calibration)")
+    ap.add_argument("--buffers", choices=("cold", "warm"), default="cold",
+                    help="prefill step inputs: cold = every layer reads its own (default), warm = one set reused by all layers")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
     args = ap.parse_args()
@@ -838,7 +840,7 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}")
 
     # ---- prefill pass (the step)
-    P = Pass(q27, torch, 2048, decode=False, cold=True)
+    P = Pass(q27, torch, 2048, decode=False, cold=args.buffers == "cold")
     step_bytes = P.bytes_per_step()
     log(f"prefill pass: {len(P.launches)} launches, {step_bytes / 1e9:.3f} GB algorithmic per step")
     for _ in range(args.warmup):
