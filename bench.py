@@ -539,6 +539,50 @@ def bench_gemv(q27, torch):
     return out
 
 
+def bench_fused_gemv(q27, torch):
+    """quantize_q8_1 + qgemv (two launches, src/model.cu:727-728 and 826-827) against q27h_qgemv_f32 (one launch) at the
+    decode shapes where the reference quantizes separately: the attention output projection (5120 x 6144) and the MTP
+    concat projection (5120 x 10240), T = 4, IQ3_S and Q4_K weights. Each timed graph holds 24 pairs (or 24 fused
+    launches) over 24 distinct matrices, so the weights come from HBM as in a decode step; median replay / 24."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(19)
+    out = {}
+    for name, (tid, bb, doffs) in (("iq3_s", GEMV_TYPES["iq3_s"]), ("q4_k", GEMV_TYPES["q4_k"])):
+        for N, K in ((5120, 6144), (5120, 10240)):
+            nc, cnt = 4, 24
+            raw = torch.randint(0, 256, (N * (K // 256), bb), dtype=torch.uint8, device=dev, generator=g)
+            for off in doffs:
+                d = torch.exp2(torch.rand(raw.shape[0], device=dev, generator=g) * 6 - 10).to(torch.float16)
+                raw[:, off:off + 2] = d.view(torch.uint8).view(-1, 2)
+            mats = [q27.ops.qmat_upload(raw.reshape(-1), tid, N, K) for _ in range(cnt)]
+            del raw
+            x = torch.randn(nc * K, device=dev, generator=g)
+            xq = torch.empty(nc * K, dtype=torch.int8, device=dev)
+            xd = torch.empty(nc * K // 32, device=dev)
+            y = torch.empty(nc * N, device=dev)
+            it = {"i": 0}
+
+            def pair():
+                m = mats[it["i"] % cnt]
+                it["i"] += 1
+                q27.ops.quantize_q8_1(x, xq, xd, K, nc)
+                q27.ops.qgemv(m, xq, xd, y, nc)
+
+            def fused():
+                m = mats[it["i"] % cnt]
+                it["i"] += 1
+                q27.ops.qgemv_f32(m, x, y, nc)
+
+            us_pair = time_graph(torch, pair, cnt)
+            us_fused = time_graph(torch, fused, cnt)
+            out[f"{name}_{N}x{K}_T{nc}"] = {"unfused_us": round(us_pair, 2), "fused_us": round(us_fused, 2)}
+            log(f"  quantize+qgemv {name} {N}x{K} T={nc}: {us_pair:6.2f} us as two launches, {us_fused:6.2f} us fused")
+            del mats
+            torch.cuda.empty_cache()
+    return out
+
+
 def bench_gdn(q27, torch, M=2048):
     """The delta-rule recurrence (gdn_step, src/ops.cu:449-572) of one GDN layer at the model's head counts (48
     value heads on 16 key heads, 128 x 128 f32 state each): prefill of M tokens in flip mode and a decode launch of
@@ -973,6 +1017,7 @@ def main():
     torch.cuda.empty_cache()
     gemv = bench_gemv(q27, torch)
     torch.cuda.empty_cache()
+    fused_gemv = bench_fused_gemv(q27, torch)
     gdn_rec = bench_gdn(q27, torch)
     upload = bench_upload(q27, torch)
 
@@ -1025,6 +1070,7 @@ def main():
         "gathers_cfg4": gathers,
         "multimodal_cfg5": multimodal,
         "decode_gemv": gemv,
+        "decode_quantize_gemv_fused": fused_gemv,
         "gdn_recurrence": gdn_rec,
         "gguf_upload": upload,
         "roofline": roofline,

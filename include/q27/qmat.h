@@ -85,6 +85,11 @@ inline void qgemv(const QMat& m, const int8_t* xq, const float* xd, float* y, in
   q27h_check(q27h_qgemv((int)m.type, m.N, m.K, m.buf, xq, xd, y, ncols, s));
 }
 
+// quantize_q8_1 + qgemv in one launch (no counterpart in the reference; see q27h_qgemv_f32): x f32 [ncols][K].
+inline void qgemv_f32(const QMat& m, const float* x, float* y, int ncols, hipStream_t s) {
+  q27h_check(q27h_qgemv_f32((int)m.type, m.N, m.K, m.buf, x, y, ncols, s));
+}
+
 // src/qmat.h:50
 inline void quantize_q8_1(const float* x, int8_t* xq, float* xd, int K, int ncols, hipStream_t s, float* xs = nullptr) {
   q27h_check(q27h_quantize_q8_1(x, xq, xd, K, ncols, s, xs));

@@ -176,6 +176,13 @@ int q27h_qmat_repack(int type, int N, int K, const void* raw, void* buf, q27h_st
  * takes 1, 2 or 4), x as q8_1 activations xq [ncols][K] (16-byte aligned), xd [ncols][K/32]. */
 int q27h_qgemv(int type, int N, int K, const void* buf, const int8_t* xq, const float* xd, float* y, int ncols,
                q27h_stream_t s);
+/* qgemv over f32 activations x [ncols][K] (16-byte aligned): no counterpart in the reference, which runs
+ * quantize_q8_1 (src/qgemv.cu:840-845) and then qgemv (src/qgemv.cu:785-801) as two launches (src/model.cu:727-728,
+ * 826-827). Every workgroup quantizes x to q8_1 in LDS with the code of q27h_quantize_q8_1, so y equals that pair's
+ * result bit for bit; one launch instead of two, for callers whose activations are f32. K * ncols <= 40960
+ * (K * 2 for three columns), else Q27H_ERR_SHAPE. Slower than the pair at the decode shapes (every workgroup
+ * quantizes the whole x): 5120 x 6144 at four columns 21-23 against 12-13 us. */
+int q27h_qgemv_f32(int type, int N, int K, const void* buf, const float* x, float* y, int ncols, q27h_stream_t s);
 /* Waves that share one 8-row tile in a q27h_qgemv launch of ncols columns (1..16; three columns run as launches of two
  * and one): part of the summation order, a function of the type, K and ncols only. */
 int q27h_qgemv_waves(int type, int K, int ncols);

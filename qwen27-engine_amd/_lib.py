@@ -67,6 +67,7 @@ SIGNATURES = {
     "q27h_qmat_bytes": [_i, _i, _i],
     "q27h_qmat_repack": [_i, _i, _i, _p, _p, _p],
     "q27h_qgemv": [_i, _i, _i, _p, _p, _p, _p, _i, _p],
+    "q27h_qgemv_f32": [_i, _i, _i, _p, _p, _p, _i, _p],
     "q27h_qgemv_waves": [_i, _i, _i],
     "q27h_gtype_block_bytes": [_i],
     "q27h_gtype_block_size": [_i],

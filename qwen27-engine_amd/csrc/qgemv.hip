@@ -681,12 +681,31 @@ constexpr int waves_per_tile(int type, int K, int ncols) {
   return w < 1 ? 1 : w > kMaxW ? 4 : w > cap ? cap : w;
 }
 
-template <int TYPE, int NC, bool NTP, bool ONE>
+// FUSED: the activations arrive as f32 (xf, [NC][K]); every workgroup first quantizes them to q8_1 in LDS with the
+// code of quantize_q8_1 (q8_1_store_n: amax, d = amax / 127, q = roundf(y / d), scale fp16(d)), then reads them from
+// there. The results are those of quantize_q8_1 followed by the unfused GEMV, bit for bit.
+constexpr int kFusedMaxX = 40960;  // NC * K values a fused launch may quantize per workgroup (40 KB of int8 in LDS)
+template <int TYPE, int NC, bool NTP, bool ONE, bool FUSED = false>
 __device__ __forceinline__ void qgemv_body(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                           float* __restrict__ y, int K, int W) {
+                                           float* __restrict__ y, int K, int W, const float* __restrict__ xf = nullptr) {
   constexpr int LW = LutInfo<TYPE>::words;
   __shared__ uint32_t lut[LW > 0 ? LW : 1];
   __shared__ float part[kMaxW][8 * NC];
+  if constexpr (FUSED) {
+    __shared__ __align__(16) int8_t s_xq[kFusedMaxX];
+    __shared__ float s_xd[kFusedMaxX / 32];
+    const int nblk = NC * K / 32;
+    const int lane8 = threadIdx.x & 7;
+    for (int b = threadIdx.x >> 3; b < nblk; b += blockDim.x >> 3) {
+      const int i0 = 32 * b + block_offset(lane8);
+      const float4 v = ld4(xf + i0);
+      const float yv[1][4] = {{v.x, v.y, v.z, v.w}};
+      q8_1_store_n<false, 1, true>(yv, s_xq, s_xd, nullptr, i0, 0);
+    }
+    xq = s_xq;
+    xd = s_xd;
+    __syncthreads();
+  }
   if constexpr (LW > 0) {
     constexpr int G = LutInfo<TYPE>::grid, NM = LutInfo<TYPE>::masks;
     for (int i = threadIdx.x; i < G; i += blockDim.x) {
@@ -808,15 +827,16 @@ __device__ __forceinline__ void qgemv_body(Mat m, const int8_t* __restrict__ xq,
 #ifndef Q27H_QG_WPE_ONE
 #define Q27H_QG_WPE_ONE 4
 #endif
-template <int TYPE, int NC, bool NTP>
+template <int TYPE, int NC, bool NTP, bool FUSED = false>
 __global__ void __launch_bounds__(256) qgemv_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                    float* __restrict__ y, int K, int W) {
-  qgemv_body<TYPE, NC, NTP, false>(m, xq, xd, y, K, W);
+                                                    float* __restrict__ y, int K, int W, const float* __restrict__ xf) {
+  qgemv_body<TYPE, NC, NTP, false, FUSED>(m, xq, xd, y, K, W, xf);
 }
-template <int TYPE, int NC>
+template <int TYPE, int NC, bool FUSED = false>
 __global__ void __launch_bounds__(64 * kMaxW) __attribute__((amdgpu_waves_per_eu(Q27H_QG_WPE_ONE)))
-qgemv_one_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, int K, int W) {
-  qgemv_body<TYPE, NC, true, true>(m, xq, xd, y, K, W);
+qgemv_one_kernel(Mat m, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, int K, int W,
+                 const float* __restrict__ xf) {
+  qgemv_body<TYPE, NC, true, true, FUSED>(m, xq, xd, y, K, W, xf);
 }
 
 int check_type(int type) {
@@ -824,25 +844,26 @@ int check_type(int type) {
   return Q27H_OK;
 }
 
-template <int TYPE, int NC>
-void launch_gemv(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, hipStream_t s) {
+template <int TYPE, int NC, bool FUSED = false>
+void launch_gemv(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, hipStream_t s, const float* xf = nullptr) {
   const int W = waves_per_tile(TYPE, K, NC);
   const int grid = m.ntiles;
   // the prefetching kernel takes at most 4 waves (lanes with several blocks); W > 4 means one block per lane
   const bool one = m.nb <= 8 * W && (W > 4 || !((TYPE == kQ2K || TYPE == kQ4K) && NC == 4));
   if (one)
-    hipLaunchKernelGGL((qgemv_one_kernel<TYPE, NC>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
+    hipLaunchKernelGGL((qgemv_one_kernel<TYPE, NC, FUSED>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W, xf);
   else if (K <= kNtPiecesMaxK)
-    hipLaunchKernelGGL((qgemv_kernel<TYPE, NC, true>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
+    hipLaunchKernelGGL((qgemv_kernel<TYPE, NC, true, FUSED>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W, xf);
   else
-    hipLaunchKernelGGL((qgemv_kernel<TYPE, NC, false>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W);
+    hipLaunchKernelGGL((qgemv_kernel<TYPE, NC, false, FUSED>), dim3(grid), dim3(64 * W), 0, s, m, xq, xd, y, K, W, xf);
 }
 
-template <int TYPE>
-void launch_nc(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, int nc, hipStream_t s) {
-  if (nc == 1) launch_gemv<TYPE, 1>(m, xq, xd, y, K, s);
-  else if (nc == 2) launch_gemv<TYPE, 2>(m, xq, xd, y, K, s);
-  else launch_gemv<TYPE, 4>(m, xq, xd, y, K, s);
+template <int TYPE, bool FUSED = false>
+void launch_nc(const Mat& m, const int8_t* xq, const float* xd, float* y, int K, int nc, hipStream_t s,
+               const float* xf = nullptr) {
+  if (nc == 1) launch_gemv<TYPE, 1, FUSED>(m, xq, xd, y, K, s, xf);
+  else if (nc == 2) launch_gemv<TYPE, 2, FUSED>(m, xq, xd, y, K, s, xf);
+  else launch_gemv<TYPE, 4, FUSED>(m, xq, xd, y, K, s, xf);
 }
 
 }  // namespace
@@ -924,4 +945,41 @@ extern "C" int q27h_qgemv(int type, int N, int K, const void* buf, const int8_t*
     run(xq, xd, y, ncols);
   }
   return check_launch("qgemv");
+}
+
+extern "C" int q27h_qgemv_f32(int type, int N, int K, const void* buf, const float* x, float* y, int ncols,
+                              q27h_stream_t s) {
+  if (int e = check_type(type)) return e;
+  if (N <= 0 || K <= 0 || N % 8 || K % 256) return fail(Q27H_ERR_SHAPE, "qgemv_f32: N % 8 and K % 256 must be 0");
+  if (ncols < 1 || ncols > 4) return fail(Q27H_ERR_SHAPE, "qgemv_f32: ncols must be 1..4");
+  if ((long)K * (ncols == 3 ? 2 : ncols) > kFusedMaxX)
+    return fail(Q27H_ERR_SHAPE, "qgemv_f32: K * ncols must be at most " + std::to_string(kFusedMaxX) + " (q8_1 activations in LDS)");
+  if (!buf || !x || !y) return fail(Q27H_ERR_ARG, "qgemv_f32: null pointer");
+  if (((uintptr_t)buf & 255u) != 0 || !aligned16(x)) return fail(Q27H_ERR_ARG, "qgemv_f32: buf needs 256-byte and x 16-byte alignment");
+  size_t off[5];
+  layout(type, N, K, off);
+  const uint8_t* b = (const uint8_t*)buf;
+  const Mat m{{b + off[0], b + off[1], b + off[2], b + off[3]}, b + off[4], N, K / 256, N / 8};
+  const hipStream_t st = stream_of(s);
+  auto run = [&](const float* xx, float* yy, int nc) {
+    switch (type) {
+      case kQ2K: launch_nc<kQ2K, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kQ4K: launch_nc<kQ4K, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kQ6K: launch_nc<kQ6K, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kIQ2XXS: launch_nc<kIQ2XXS, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kIQ2XS: launch_nc<kIQ2XS, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kIQ3XXS: launch_nc<kIQ3XXS, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kIQ3S: launch_nc<kIQ3S, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kIQ2S: launch_nc<kIQ2S, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      case kIQ1M: launch_nc<kIQ1M, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+      default: launch_nc<kIQ4XS, true>(m, nullptr, nullptr, yy, K, nc, st, xx); break;
+    }
+  };
+  if (ncols == 3) {
+    run(x, y, 2);
+    run(x + (size_t)2 * K, y + (size_t)2 * N, 1);
+  } else {
+    run(x, y, ncols);
+  }
+  return check_launch("qgemv_f32");
 }

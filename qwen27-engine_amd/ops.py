@@ -223,5 +223,10 @@ def qgemv(m, xq, xd, y, ncols, s=None):
     check(lib().q27h_qgemv(m.type, m.N, m.K, _ptr(m.buf), _ptr(xq), _ptr(xd), _ptr(y), ncols, _stream(s)))
 
 
+def qgemv_f32(m, x, y, ncols, s=None):
+    """quantize_q8_1 of x (f32 [ncols][K]) and qgemv in one launch (q27h_qgemv_f32)."""
+    check(lib().q27h_qgemv_f32(m.type, m.N, m.K, _ptr(m.buf), _ptr(x), _ptr(y), ncols, _stream(s)))
+
+
 def qgemv_waves(type_, K, ncols):
     return int(lib().q27h_qgemv_waves(type_, K, ncols))

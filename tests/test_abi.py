@@ -148,6 +148,12 @@ def test_qgemv_rejects_before_enqueue(q27):
     assert L.q27h_qgemv(12, 64, 300, FAKE, FAKE, FAKE, FAKE, 1, None) == -1  # K % 256
     assert L.q27h_qgemv(12, 64, 256, FAKE, FAKE, FAKE, FAKE, 5, None) == -1  # ncols
     assert L.q27h_qgemv(12, 64, 256, FAKE + 16, FAKE, FAKE, FAKE, 1, None) == -4  # buf alignment
+    # the fused form: the same checks, and at most 40960 activations in LDS
+    assert L.q27h_qgemv_f32(8, 64, 256, FAKE, FAKE, FAKE, 1, None) == -2
+    assert L.q27h_qgemv_f32(12, 64, 300, FAKE, FAKE, FAKE, 1, None) == -1
+    assert L.q27h_qgemv_f32(12, 64, 256, FAKE, FAKE, FAKE, 0, None) == -1
+    assert L.q27h_qgemv_f32(12, 64, 17408, FAKE, FAKE, FAKE, 4, None) == -1  # 69632 activations
+    assert L.q27h_qgemv_f32(12, 64, 256, FAKE + 16, FAKE, FAKE, 1, None) == -4
     assert L.q27h_qmat_repack(14, 64, 256, FAKE, FAKE + 8, None) == -4
     assert L.q27h_qmat_repack(21, 64, 250, FAKE, FAKE, None) == -1
     # bytes: fields then scales, each 256-byte aligned (Q4_K 128 + 16 per chunk, 32 per (tile, block)); ntb at K = 512

@@ -140,3 +140,34 @@ def test_qgemv_lm_head_shape(q27, oracle, dev, type_):
     got = _run(q27, dev, type_, N, K, raw, xq, xd, 1)
     want = oracle.qgemv(type_, raw, N, K, xq, xd, 1)
     assert_bits_equal(got, want, f"qgemv LM head type {type_}")
+
+
+@pytest.mark.parametrize("type_", TYPES)
+@pytest.mark.parametrize("shape,ncols", [((5120, 6144), 4), ((5120, 10240), 4), ((1024, 5120), 3), ((6144, 5120), 2),
+                                         ((256, 40960), 1), ((8, 256), 1)])
+def test_qgemv_f32_equals_quantize_then_qgemv(q27, oracle, dev, type_, shape, ncols):
+    """The fused launch (q8_1 in LDS per workgroup) against quantize_q8_1 followed by qgemv, both through the C ABI,
+    and against the CPU oracle: bit-exact y."""
+    import torch
+
+    N, K = shape
+    say(f"qgemv_f32 type {type_} N={N} K={K} ncols={ncols}")
+    r = cd.rng(900 + type_ + N + K + ncols)
+    raw = cd.random_weights(r, type_, N, K)
+    x = (r.standard_normal(ncols * K) * np.exp(r.standard_normal(ncols * K) * 0.5)).astype(np.float32)
+    x[r.choice(x.size, 7, replace=False)] = 0.0
+    x[:32] = 0.0  # an all-zero block: q = 0, scale 0
+    m = q27.ops.qmat_upload(torch.from_numpy(raw).to(dev), type_, N, K)
+    dx = torch.from_numpy(x).to(dev)
+    y_f = torch.full((ncols * N,), float("nan"), device=dev)
+    q27.ops.qgemv_f32(m, dx, y_f, ncols)
+    xq = torch.zeros(ncols * K, dtype=torch.int8, device=dev)
+    xd = torch.zeros(ncols * K // 32, device=dev)
+    q27.ops.quantize_q8_1(dx, xq, xd, K, ncols)
+    y_u = torch.full((ncols * N,), float("nan"), device=dev)
+    q27.ops.qgemv(m, xq, xd, y_u, ncols)
+    torch.cuda.synchronize()
+    assert_bits_equal(y_f.cpu().numpy(), y_u.cpu().numpy(), "y (fused vs quantize + qgemv)")
+    oq, od, _ = oracle.quantize_q8_1(x, K, ncols)
+    want = oracle.qgemv(type_, raw, N, K, oq, od, ncols)
+    assert_bits_equal(y_f.cpu().numpy().reshape(ncols, N), np.asarray(want).reshape(ncols, N), "y (oracle)")
