@@ -284,10 +284,11 @@ def _cpu_shared(seed=5):
     return {"table": table, "cdf": cdf, "perm": r.permutation(VOCAB), "kc": kc, "vc": np.zeros_like(kc)}
 
 
-def _cpu_pass(M, seed, sh, pos0):
+def _cpu_pass(M, seed, sh, pos0, per_op=None):
     """The CPU oracle (scalar C) over the 322 launches of one prefill pass restricted to M token rows at the GPU
     pass's shapes (Zipf ids into the full IQ2_S table, cache rows pos0 .. pos0 + M - 1 of a 180224-row q8_0 cache).
-    Returns the algorithmic bytes it moved (the same per-row definitions as the GPU step)."""
+    Returns the algorithmic bytes it moved (the same per-row definitions as the GPU step). per_op, if given,
+    accumulates op -> [seconds, bytes]."""
     import numpy as np
 
     sys.path.insert(0, ROOT)
@@ -305,27 +306,35 @@ def _cpu_pass(M, seed, sh, pos0):
     ids = sh["perm"][np.minimum(np.searchsorted(sh["cdf"], r.random(M)), VOCAB - 1)].astype(np.int32)
     ts = float(np.float32(1e7) ** np.float32(-2.0 / 64))
     total = 0
-    O.get_rows("iq2_s", sh["table"], 1640, ids, E)
-    total += bytes_get_rows(M, len(np.unique(ids)), 1640)
-    O.rmsnorm_q8(x, w, E, M, EPS, with_h=True, with_xs=True)
-    total += bytes_rmsnorm_q8(M, True, True)
+
+    def run(name, nbytes, fn):
+        nonlocal total
+        t0 = time.perf_counter()
+        fn()
+        if per_op is not None:
+            acc = per_op.setdefault(name, [0.0, 0])
+            acc[0] += time.perf_counter() - t0
+            acc[1] += nbytes
+        total += nbytes
+
+    run("get_rows_iq2_s", bytes_get_rows(M, len(np.unique(ids)), 1640), lambda: O.get_rows("iq2_s", sh["table"], 1640, ids, E))
+    run("rmsnorm_q8", bytes_rmsnorm_q8(M, True, True), lambda: O.rmsnorm_q8(x, w, E, M, EPS, with_h=True, with_xs=True))
     for il in range(N_LAYER):
         if not is_attn(il):
-            O.gdn_conv_prefill(qkv, cw, planes, 0, C, M, 2 * KH, EPS, ab[:M * HV], ab[M * HV:], sa, dtb, HV)
-            O.gated_rmsnorm_q8(o, w128, z, M * HV, EPS, with_xs=True)
-            total += bytes_gdn_conv(M) + bytes_gated(M * HV, True)
+            run("gdn_conv_prefill", bytes_gdn_conv(M),
+                lambda: O.gdn_conv_prefill(qkv, cw, planes, 0, C, M, 2 * KH, EPS, ab[:M * HV], ab[M * HV:], sa, dtb, HV))
+            run("gated_rmsnorm_q8", bytes_gated(M * HV, True), lambda: O.gated_rmsnorm_q8(o, w128, z, M * HV, EPS, with_xs=True))
         else:
-            O.attn_prep(qg, k, v, qw, kw, sh["kc"], sh["vc"], pos0, M, EPS, ts, NQH, NKVH, N_CTX, True)
-            O.quantize_q8_1(attn_o, NQH * 256, M, with_xs=True)
-            total += bytes_attn_prep(M) + bytes_quantize(M * NQH * 256, True)
-        O.sum_norm_rows(x, part, w, E, M, EPS)
-        O.swiglu_q8(g, u, with_xs=True)
-        O.sum_norm_rows(x, part, w, E, M, EPS)
-        total += 2 * bytes_sum_norm(M, False, True) + bytes_swiglu_q8(M * FF, True)
+            run("attn_prep", bytes_attn_prep(M),
+                lambda: O.attn_prep(qg, k, v, qw, kw, sh["kc"], sh["vc"], pos0, M, EPS, ts, NQH, NKVH, N_CTX, True))
+            run("quantize_q8_1", bytes_quantize(M * NQH * 256, True), lambda: O.quantize_q8_1(attn_o, NQH * 256, M, with_xs=True))
+        run("sum_norm_rows", bytes_sum_norm(M, False, True), lambda: O.sum_norm_rows(x, part, w, E, M, EPS))
+        run("swiglu_q8", bytes_swiglu_q8(M * FF, True), lambda: O.swiglu_q8(g, u, with_xs=True))
+        run("sum_norm_rows", bytes_sum_norm(M, False, True), lambda: O.sum_norm_rows(x, part, w, E, M, EPS))
     return total
 
 
-def cpu_baseline(rows, threads, sh):
+def cpu_baseline(rows, threads, sh, per_op=None):
     """The oracle on a bounded sample of the prefill pass: `rows` token rows split over `threads` host threads (the
     C calls release the GIL), each thread on its own rows and cache positions. Returns (GB/s, seconds)."""
     from concurrent.futures import ThreadPoolExecutor
@@ -333,7 +342,7 @@ def cpu_baseline(rows, threads, sh):
     per = max(1, rows // threads)
     t0 = time.perf_counter()
     if threads == 1:
-        total = _cpu_pass(per, 5, sh, 131072)
+        total = _cpu_pass(per, 5, sh, 131072, per_op)
     else:
         with ThreadPoolExecutor(threads) as ex:
             total = sum(ex.map(lambda i: _cpu_pass(per, 5 + i, sh, 131072 + i * per), range(threads)))
@@ -1036,7 +1045,8 @@ def main():
         share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or hw["affinity_cpus"]
         threads = max(1, min(share, hw["affinity_cpus"]))
         sh = _cpu_shared()
-        gbs1, secs1 = cpu_baseline(max(1, args.cpu_rows // threads), 1, sh)
+        cpu_ops = {}
+        gbs1, secs1 = cpu_baseline(max(1, args.cpu_rows // threads), 1, sh, cpu_ops)
         gbsn, secsn = cpu_baseline(args.cpu_rows, threads, sh)
         cpu = {"value": round(gbsn, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": (f"the prefill pass (64 layers, 322 launches of the oracle) on {args.cpu_rows} token rows split over "
@@ -1044,6 +1054,7 @@ def main():
                           f"table, q8_0 cache of 180224 rows at pos0 131072): {secsn:.1f} s; single thread on "
                           f"{max(1, args.cpu_rows // threads)} rows: {gbs1:.3f} GB/s ({secs1:.1f} s)"),
                "single_thread_GBps": round(gbs1, 3),
+               "single_thread_per_op": {k: {"GBps": round(b / t / 1e9, 3), "s": round(t, 3)} for k, (t, b) in cpu_ops.items()},
                "host": hw,
                "us_per_2048_batch_equiv": round(step_bytes / (gbsn * 1e9) * 1e6, 0)}
         log(f"cpu oracle: {gbsn:.3f} GB/s on {threads} threads ({secsn:.1f} s), {gbs1:.3f} GB/s on 1 thread ({secs1:.1f} s); {hw}")
