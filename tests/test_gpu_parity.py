@@ -390,6 +390,15 @@ def test_attn_prep(q27, oracle, T, Tn, pos0, q8, rdelta):
     run_attn_pair(q27, oracle, T, Tn, pos0, cd.N_CTX, q8, 90 + Tn, rdelta=rdelta)
 
 
+@pytest.mark.parametrize("Tn,pos0,q8,rdelta", [(74, 0, False, None), (75, 180224 - 40, True, None), (2048, 7, False, None),
+                                               (513, 100000, True, 9)])
+def test_attn_prep_token_workgroups(q27, oracle, T, Tn, pos0, q8, rdelta):
+    # launches of T * 28 >= 2048 heads take one workgroup per token (angles shared through LDS): f16 and q8_0 caches,
+    # rows past n_ctx, an rdelta shift and odd token counts
+    say(f"attn_prep (workgroup per token) T={Tn} pos0={pos0} q8={q8} rdelta={rdelta}")
+    run_attn_pair(q27, oracle, T, Tn, pos0, cd.N_CTX, q8, 700 + Tn, rdelta=rdelta)
+
+
 def test_attn_prep_imrope_cfg5(q27, oracle, T):
     say("attn_prep cfg5 IMRoPE 4099 rows")
     rope3 = cd.rope3_grid()
