@@ -26,7 +26,13 @@ __device__ __forceinline__ float lane_xor(float v) {
   else if constexpr (M == 2) r = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
   else if constexpr (M == 8) r = __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, true);  // row_ror:8 (16-lane rows)
   else if constexpr (M == 7) r = __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, true);  // row_half_mirror: l ^ 7 in 8
-  else r = __builtin_amdgcn_ds_swizzle(iv, (M << 10) | 0x1F);                          // bit mode: lane ^ M
+  else if constexpr (M == 16) {
+    // v_permlane16_swap of a value with itself: the first result holds row 0 in rows 0 and 1 (row 2 in rows 2 and 3),
+    // the second row 1 in rows 0 and 1 (row 3 in rows 2 and 3), so the partner row of lane l is the second result
+    // for l & 16 == 0 and the first otherwise (a VALU exchange, no LDS round trip)
+    const auto pr = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    r = (__lane_id() & 16) ? (int)pr[0] : (int)pr[1];
+  } else r = __builtin_amdgcn_ds_swizzle(iv, (M << 10) | 0x1F);                        // bit mode: lane ^ M
   return __builtin_bit_cast(float, r);
 }
 // Value of lane ((lane & AND) | OR) inside the same 32-lane group (ds_swizzle bit mode).
