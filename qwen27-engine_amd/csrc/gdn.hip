@@ -12,7 +12,7 @@
 #include "q27h_internal.h"
 
 #ifndef Q27H_GDN_SPAN
-#define Q27H_GDN_SPAN 8
+#define Q27H_GDN_SPAN 4
 #endif
 
 namespace q27h {
@@ -67,7 +67,9 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
 // registers. The gates (sigmoid / softplus of the H value heads of every token) are not evaluated by the conv lanes:
 // the first `gate_blocks` workgroups of the grid take one (token, value head) per lane. Workgroups that walk 16-64
 // consecutive tokens of a head group (the window carried in registers, the next span's rows prefetched) measured
-// slower: 41-54 against 37.4 us at M = 2048.
+// slower: 41-54 against 37.4 us at M = 2048. Spans of 4 tokens (64 VGPRs, 8 waves per SIMD) measured 37.2 us against
+// 39.2 / 37.3 / 37.9 us for spans of 3 / 5 / 8 and 10.43-10.46 against 10.47-10.54 ms per prefill pass for 8; the
+// token loop without a branch per token (the out-of-range silu redone after the stores) measured the same (37.1 us).
 template <int SPAN>
 __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __restrict__ x, const float* __restrict__ cw,
                                                                float* __restrict__ planes, const int* __restrict__ in_plane,
