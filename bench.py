@@ -974,6 +974,11 @@ def main():
                 "frac": round(sw_gbs / HBM_PEAK_GBS, 4), "traffic": SWIGLU_TRAFFIC_BYTES, "kernel": "swiglu_q8 (flat_q8_kernel<true>)",
                 "bytes_per_launch": sw_bytes, "avg_launch_us": round(sw_us, 2),
                 "note": "2048 x 17408 values, 9.375 B each (g, u f32 in; xq int8, xd f32 per 32, xs f32 per 16 out)"}
+    # sum_norm_rows takes as long per pass as swiglu_q8 (128 launches of half the time); its isolated figure beside it
+    sn = isolated["sum_norm_rows"]
+    roofline["co_dominant"] = {"kernel": "sum_norm_rows (row_norm_q8_kernel<1>)", "achieved": sn["GBps"],
+                               "frac": round(sn["GBps"] / HBM_PEAK_GBS, 4), "avg_launch_us": sn["us"],
+                               "bytes_per_launch": sn["bytes_per_launch"], "launches_per_pass": sn["launches"]}
     # ---- practical copy ceiling of this device (torch device-to-device copy of 512 MiB, read + write bytes)
     src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
