@@ -622,6 +622,17 @@ def bench_gdn(q27, torch, M=2048):
         out[name] = {"us": round(us, 2), "tokens": T, "us_per_token": round(us / T, 3), "GBps": round(b / us / 1e3, 1),
                      "MB": round(b / 1e6, 2)}
         log(f"  gdn_step {name:9s} T={T:5d} {us:8.2f} us ({us / T:.3f} us/token) {b / us / 1e3:7.1f} GB/s")
+        if flip:  # the chunked form on matrix cores, same inputs
+            def fc(i=0):
+                q27.ops.gdn_step_chunked(x, x[HK * D:], x[2 * HK * D:], stride, gg, beta, planes, pin, o, H, HK, T, 0.0884)
+
+            uc = time_back_to_back(torch, fc, 20)
+            # multiply-adds of the three state products (K S, Q S, K^T Delta) per token and head, as fp32 MFMA work
+            tf = 3 * 2 * D * D * T * H / (uc * 1e-6) / 1e12
+            out[name + "_chunked"] = {"us": round(uc, 2), "tokens": T, "us_per_token": round(uc / T, 3),
+                                      "GBps": round(b / uc / 1e3, 1), "state_products_TFLOPs": round(tf, 2)}
+            log(f"  gdn_step {name + '_chunked':9s} T={T:5d} {uc:8.2f} us ({uc / T:.3f} us/token), state products "
+                f"{tf:.1f} TFLOP/s")
     return out
 
 

@@ -77,6 +77,12 @@ def gdn_step(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, sna
                               _ptr(o), H, HK, T, scale, int(snapshots), _stream(s), int(flip)))
 
 
+def gdn_step_chunked(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, s=None):
+    """gdn_step's prefill (flip) mode in the chunked form on matrix cores (no counterpart in the reference)."""
+    check(lib().q27h_gdn_step_chunked(_ptr(q), _ptr(k), _ptr(v), stride, _ptr(g), _ptr(beta), _ptr(planes),
+                                      _ptr(in_plane), _ptr(o), H, HK, T, scale, _stream(s)))
+
+
 def l2norm_heads(x, n, heads, T, stride, eps, s=None):
     check(lib().q27h_l2norm_heads(_ptr(x), n, heads, T, stride, eps, _stream(s)))
 

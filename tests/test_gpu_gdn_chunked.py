@@ -1,0 +1,105 @@
+"""GPU checks of the chunked prefill form of the delta rule (q27h_gdn_step_chunked through the C ABI): o and the
+final state against the sequential CPU oracle (itself pinned bit for bit against the sequential GPU kernel and by a
+float64 recurrence) within float32 rounding, relative 1e-5 of the largest value (the north_star's fp32 tolerance),
+and against a float64 recurrence; plane semantics bit for bit (only the other of planes 0 / 1 is written)."""
+import sys
+
+import numpy as np
+import pytest
+
+import cfgdata as cd
+
+pytestmark = pytest.mark.gpu
+
+SCALE = np.float32(1.0 / np.sqrt(128.0))
+RTOL = 1e-5  # of the largest |value| of the compared array
+
+
+def say(msg):
+    print(f"[gpu-gdn-chunked] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _run(q27, dev, x, stride, g, beta, planes, in_plane, H, HK, T):
+    import torch
+
+    dx = torch.from_numpy(x).to(dev)
+    dp = torch.from_numpy(planes).to(dev)
+    pin = torch.tensor([in_plane], dtype=torch.int32, device=dev)
+    o = torch.full((max(T, 1) * H * 128,), float("nan"), device=dev)
+    q27.ops.gdn_step_chunked(dx, dx[HK * 128:], dx[2 * HK * 128:], stride, torch.from_numpy(g).to(dev),
+                             torch.from_numpy(beta).to(dev), dp, pin, o, H, HK, T, float(SCALE))
+    torch.cuda.synchronize()
+    return o.cpu().numpy()[: T * H * 128], dp.cpu().numpy()
+
+
+def _close(got, want, what):
+    assert np.all(np.isfinite(got)), f"{what}: non-finite values"
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
+    ref = np.abs(want.astype(np.float64)).max()
+    assert err <= RTOL * ref, f"{what}: max error {err:.3e} > {RTOL} x {ref:.3e}"
+    return err / ref
+
+
+def _f64_recurrence(x, stride, g, beta, planes, in_plane, H, HK, T):
+    """The delta rule in float64 (delta = (v - e^g S^T k) beta, S <- e^g S + k delta^T, o = scale S^T q)."""
+    S = planes.reshape(4, H, 128, 128)[in_plane].astype(np.float64).transpose(0, 2, 1).copy()  # [h][i][col]
+    X = x.reshape(T, stride).astype(np.float64)
+    kh = np.arange(H) % HK
+    o = np.empty((T, H, 128))
+    for t in range(T):
+        q = X[t, : HK * 128].reshape(HK, 128)[kh]
+        k = X[t, HK * 128: 2 * HK * 128].reshape(HK, 128)[kh]
+        v = X[t, 2 * HK * 128:].reshape(H, 128)
+        e = np.exp(g[t * H: (t + 1) * H].astype(np.float64))[:, None]
+        kv = np.einsum("hi,hic->hc", k, S)
+        d = (v - e * kv) * beta[t * H: (t + 1) * H].astype(np.float64)[:, None]
+        S = e[:, :, None] * S + k[:, :, None] * d[:, None, :]
+        o[t] = np.einsum("hi,hic->hc", q, S) * float(SCALE)
+    return o.reshape(-1), S.transpose(0, 2, 1).reshape(-1)
+
+
+@pytest.mark.parametrize("M,in_plane", [(2048, 0), (333, 1), (17, 0), (16, 1), (5, 0), (1, 1)])
+def test_gdn_chunked_vs_sequential_oracle(q27, oracle, dev, M, in_plane):
+    H, HK = cd.HV, cd.KH
+    say(f"gdn chunked M={M} in_plane={in_plane}")
+    x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(200 + M), M)
+    got_o, got_p = _run(q27, dev, x, stride, g, beta, planes, in_plane, H, HK, M)
+    want_o, want_p = oracle.gdn_step(x, x[HK * 128:], x[2 * HK * 128:], stride, g, beta, planes, in_plane, H, HK, M,
+                                     SCALE, False, True)
+    out = 1 if in_plane == 0 else 0
+    n = H * 128 * 128
+    _close(got_o, want_o, f"o M={M}")
+    _close(got_p[out * n:(out + 1) * n], want_p[out * n:(out + 1) * n], f"final state M={M}")
+    for p in range(4):  # every other plane untouched, bit for bit
+        if p != out:
+            assert np.array_equal(got_p[p * n:(p + 1) * n].view(np.uint32), planes[p * n:(p + 1) * n].view(np.uint32)), p
+
+
+@pytest.mark.parametrize("M", [333, 40])
+def test_gdn_chunked_vs_float64(q27, dev, M):
+    H, HK = cd.HV, cd.KH
+    say(f"gdn chunked vs float64 M={M}")
+    x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(400 + M), M)
+    got_o, got_p = _run(q27, dev, x, stride, g, beta, planes, 0, H, HK, M)
+    want_o, want_s = _f64_recurrence(x, stride, g, beta, planes, 0, H, HK, M)
+    n = H * 128 * 128
+    _close(got_o, want_o, f"o vs float64 M={M}")
+    _close(got_p[n:2 * n], want_s, f"state vs float64 M={M}")
+
+
+def test_gdn_chunked_edge_values(q27, oracle, dev):
+    """HK = H = 5, beta 0 / 1, g = 0 and -60 (decays that underflow inside a chunk), larger state values."""
+    H, HK, M = 5, 5, 70
+    say(f"gdn chunked edge H={H} HK={HK} M={M}")
+    x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(300), M, H, HK, planes_std=3.0)
+    beta[::7] = 0
+    beta[1::7] = 1
+    g[::5] = 0
+    g[2::5] = -60
+    got_o, got_p = _run(q27, dev, x, stride, g, beta, planes, 0, H, HK, M)
+    want_o, want_p = oracle.gdn_step(x, x[HK * 128:], x[2 * HK * 128:], stride, g, beta, planes, 0, H, HK, M, SCALE,
+                                     False, True)
+    n = H * 128 * 128
+    _close(got_o, want_o, "edge o")
+    _close(got_p[n:2 * n], want_p[n:2 * n], "edge state")
