@@ -5,18 +5,25 @@
 // Per value head h and chunk of C = 16 tokens (G_c = g_0 + ... + g_c, gamma_c = e^G_c, D_cs = e^(G_c - G_s)):
 //   A     = strictly lower part of beta_c D_cs (k_c . k_s)            (C x C)
 //   Tinv  = (I + A)^-1 = (I - A)(I + A^2)(I + A^4)(I + A^8)          (A^16 = 0)
+//   M     = lower part, diagonal included, of D_cs (q_c . k_s)
 //   Delta = Tinv (beta (V - gamma (K S)))                              (C x cols: the tokens' delta vectors)
-//   O     = scale (gamma (Q S) + (lower part incl. diagonal of D (Q K^T)) Delta)
+//   O     = scale (gamma (Q S) + M Delta)
 //   S    <- gamma_15 S + sum_s D_15,s k_s Delta_s^T
 // which unrolls the per-token rule  delta = (v - e^g S^T k) beta,  S <- e^g S + k delta^T,  o = scale S^T q  over the
 // chunk (the sequential kernel's comment gives the per-token form).
 //
-// gfx950 layout: a 512-thread workgroup = one value head and 32 value columns (grid H x 4); wave w holds the state
-// rows 32 (w & 3) .. + 31 of the columns 16 (w >> 2) .. + 15 of the workgroup as two 16 x 16 accumulator tiles of
-// v_mfma_f32_16x16x4_f32 (lane l: rows 4 (l / 16) + i, column l % 16). Every product is a 16 x 16 x 4 MFMA: K K^T and
-// Q K^T split over the 8 waves by key (16 keys each), K S and Q S over the 4 row groups of a column half, the 16 x 16
-// products of the inverse on one wave. Operands whose rows are the MFMA's K dimension are read in the state tile's
-// own row order (key 16 b + 4 (l / 16) + i at step i), so the state is never moved out of its accumulators.
+// Two launches. gdn_chunk_prep_kernel (one wave per value head and chunk, all chunks in parallel) forms Tinv and M,
+// which do not depend on the state, and parks them where the second launch finds them: for a full chunk in the
+// chunk's own rows of o (one 16 x 32 copy per 32-column group of the head, [t][j] = Tinv[t][j] for j < 16, M[t][j - 16]
+// otherwise), which the recurrence overwrites only with that group's own outputs after reading them; for a last,
+// partial chunk in the output state plane (keys 0..15 of the group's 32 columns), written only at the very end.
+// gdn_chunk_kernel then walks the chunks of one value head and 32 value columns (grid H x 4, 512 threads): wave w
+// holds the state rows 32 (w & 3) .. + 31 of the columns 16 (w >> 2) .. + 15 as two 16 x 16 accumulator tiles of
+// v_mfma_f32_16x16x4_f32 (lane l: rows 4 (l / 16) + i, column l % 16). K S and Q S are split over the 4 row groups of
+// a column half (their operand steps read keys in the state tile's own row order, so the state never leaves its
+// accumulators); Delta and O are formed by one wave per column half, with the 16 x 16 right-hand side turned into
+// MFMA operands by lane swaps; the update is an MFMA into the state tiles. A chunk's rows (k, q, v, g, beta, Tinv, M)
+// are loaded three chunks ahead into one of four LDS buffers.
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
@@ -25,38 +32,12 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kC = 16;     // tokens per chunk
-constexpr int kNC = 32;    // value columns per workgroup
-constexpr int kKP = 132;   // padded LDS row of the chunk's k / q (floats)
+constexpr int kNC = 32;    // value columns per workgroup of the recurrence
+constexpr int kKP = 132;   // padded LDS row of a chunk's k / q (floats)
 constexpr int kMP = 17;    // padded LDS row of the 16 x 16 matrices
 
 __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// LDS writes of this wave visible to its own later LDS reads (other lanes' addresses)
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Z = (X + ix I)(Y + iy I) for 16 x 16 matrices in LDS, by one wave; Z in the accumulator layout.
-__device__ __forceinline__ v4f mm16(const float (*X)[kMP], const float (*Y)[kMP], bool ix, bool iy, int l) {
-  const int r = l & 15, kq = l >> 4;
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int m = 0; m < 4; m++) {
-    const int kk = 4 * m + kq;
-    const float a = X[r][kk] + (ix && r == kk ? 1.0f : 0.0f);
-    const float b = Y[kk][r] + (iy && r == kk ? 1.0f : 0.0f);
-    acc = mfma4(a, b, acc);
-  }
-  return acc;
-}
-__device__ __forceinline__ void put16(float (*Z)[kMP], v4f z, int l) {
-  const int r = l & 15, kq = l >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; i++) Z[4 * kq + i][r] = z[i];
 }
 
 // A 16 x 16 tile in the accumulator layout (lane l = (g, c), g = l / 16: rows 4 g .. 4 g + 3 of column c) to the
@@ -87,30 +68,155 @@ __device__ __forceinline__ v4f tile_to_operand(v4f x) {
   return y;
 }
 
+// X Y^T of two 16 x 128 row blocks in LDS over all 128 columns, by one wave, in the accumulator layout. MFMA step m
+// takes column 16 (m / 4) + 4 (l / 16) + m % 4 on both operands (16-byte reads), four accumulators keep the steps
+// independent.
+__device__ __forceinline__ v4f gram16(const float (*X)[kKP], const float (*Y)[kKP], int r, int kq) {
+  v4f acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const float4 x4 = *(const float4*)&X[r][16 * j + 4 * kq];
+    const float4 y4 = *(const float4*)&Y[r][16 * j + 4 * kq];
+    acc[0] = mfma4(x4.x, y4.x, acc[0]);
+    acc[1] = mfma4(x4.y, y4.y, acc[1]);
+    acc[2] = mfma4(x4.z, y4.z, acc[2]);
+    acc[3] = mfma4(x4.w, y4.w, acc[3]);
+  }
+  return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+// G_t = g_0 + ... + g_t (token order) on lane t < 16 (lanes >= 16: the sum of all 16), g[16] in LDS, 16-byte aligned
+__device__ __forceinline__ float prefix16(const float* g, int l) {
+  float gv[kC];
+#pragma unroll
+  for (int j = 0; j < kC; j += 4) {  // read unconditionally (a select per term, not a masked read per term)
+    const float4 g4 = *(const float4*)&g[j];
+    gv[j] = g4.x; gv[j + 1] = g4.y; gv[j + 2] = g4.z; gv[j + 3] = g4.w;
+  }
+  float G = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kC; j++) G += j <= l ? gv[j] : 0.0f;
+  return G;
+}
+
+// (I + B)^-1 = (I + B)(I + B^2)(I + B^4)(I + B^8) for strictly lower B [16][kMP] in LDS, by one wave, in registers:
+// every product Z = X Y is formed with its transpose (Z^T = Y^T X^T, a second MFMA chain), both turned into B-operand
+// tiles, so the next product reads both operands from registers (the A operand of X is the B operand of X^T).
+// Result in the accumulator layout.
+__device__ __forceinline__ v4f unit_lower_inverse(const float (*B)[kMP], int r, int kq) {
+  v4f bB, bBt;  // B-operand tiles of B and B^T
+#pragma unroll
+  for (int m = 0; m < 4; m++) {
+    bB[m] = B[4 * m + kq][r];
+    bBt[m] = B[r][4 * m + kq];
+  }
+  auto addI = [&](v4f x) {  // (I + X) in the B-operand layout: step m holds row 4 m + kq of column r
+#pragma unroll
+    for (int m = 0; m < 4; m++) x[m] += (4 * m + kq == r) ? 1.0f : 0.0f;
+    return x;
+  };
+  auto mm = [&](v4f xt, v4f y) {  // Z = X Y from the B-operand tiles of X^T and Y; Z in the accumulator layout
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; m++) acc = mfma4(xt[m], y[m], acc);
+    return acc;
+  };
+  const v4f b2 = tile_to_operand(mm(bBt, bB)), b2t = tile_to_operand(mm(bB, bBt));
+  const v4f b4 = tile_to_operand(mm(b2t, b2)), b4t = tile_to_operand(mm(b2, b2t));
+  const v4f p1t = tile_to_operand(mm(addI(b2), addI(bBt)));  // ((I + B)(I + B^2))^T = (I + B^2^T)(I + B^T)
+  const v4f b8 = tile_to_operand(mm(b4t, b4));
+  const v4f p2t = tile_to_operand(mm(addI(b4), p1t));  // ((I + B)(I + B^2)(I + B^4))^T
+  return mm(p2t, addI(b8));
+}
+
+// ---------------------------------------------------------------- prep: Tinv and M of every chunk
+__global__ void __launch_bounds__(64) gdn_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                            int stride, const float* __restrict__ g,
+                                                            const float* __restrict__ beta, float* __restrict__ planes,
+                                                            const int* __restrict__ in_plane, float* __restrict__ o,
+                                                            int H, int HK, int T) {
+  __shared__ __align__(16) float sK[kC][kKP];
+  __shared__ __align__(16) float sQ[kC][kKP];
+  __shared__ __align__(16) float sg[kC];
+  __shared__ float sb[kC];
+  __shared__ float sB[kC][kMP];
+  const int h = blockIdx.x, c = blockIdx.y, kh = h % HK;
+  const int c0 = c * kC, n = min(kC, T - c0);
+  const int l = threadIdx.x, r = l & 15, kq = l >> 4;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int e = l + 64 * j, t = e >> 5, e4 = (e & 31) * 4;
+    float4 kv4 = make_float4(0.f, 0.f, 0.f, 0.f), qv4 = kv4;
+    if (t < n) {
+      kv4 = ld4(k + (size_t)(c0 + t) * stride + kh * 128 + e4);
+      qv4 = ld4(q + (size_t)(c0 + t) * stride + kh * 128 + e4);
+    }
+    *(float4*)&sK[t][e4] = kv4;
+    *(float4*)&sQ[t][e4] = qv4;
+  }
+  if (l < kC) {
+    sg[l] = l < n ? g[(size_t)(c0 + l) * H + h] : 0.0f;
+    sb[l] = l < n ? beta[(size_t)(c0 + l) * H + h] : 0.0f;
+  }
+  __syncthreads();
+  const v4f kk = gram16(sK, sK, r, kq), qk = gram16(sQ, sK, r, kq);
+  const float Gt = prefix16(sg, l);
+  const float Gs = __shfl(Gt, r, 64);
+  v4f mt;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int cc = 4 * kq + i;
+    const float Gc = __shfl(Gt, cc, 64);  // every lane takes part (a lane exchange reads from active lanes only)
+    const float d = r <= cc ? q27_expf(Gc - Gs) : 0.0f;
+    sB[cc][r] = r < cc ? -((sb[cc] * d) * kk[i]) : 0.0f;
+    mt[i] = r <= cc ? d * qk[i] : 0.0f;
+  }
+  __syncthreads();
+  const v4f ti = unit_lower_inverse(sB, r, kq);
+  const size_t plane_sz = (size_t)H * 128 * 128;
+  const int pout = *in_plane == 0 ? 1 : 0;
+#pragma unroll
+  for (int cg = 0; cg < 128 / kNC; cg++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int t = 4 * kq + i;
+      if (n == kC) {
+        float* dst = o + ((size_t)(c0 + t) * H + h) * 128 + kNC * cg;
+        dst[r] = ti[i];
+        dst[16 + r] = mt[i];
+      } else {
+        float* dst = planes + (size_t)pout * plane_sz + ((size_t)h * 128 + kNC * cg) * 128 + t;
+        dst[(size_t)r * 128] = ti[i];
+        dst[(size_t)(16 + r) * 128] = mt[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- the recurrence over the chunks
 __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                         const float* __restrict__ v, int stride,
                                                         const float* __restrict__ g, const float* __restrict__ beta,
                                                         float* __restrict__ planes, const int* __restrict__ in_plane,
                                                         float* __restrict__ o, int H, int HK, int T, float scale) {
-  // chunk rows, four buffers (chunk n in use, n + 1 and n + 2 being prepared, n + 3 arriving)
+  // a chunk's rows, four buffers (chunk n in use, n + 1 and n + 2 waiting, n + 3 arriving)
   __shared__ __align__(16) float sKb[4][kC][kKP];
   __shared__ __align__(16) float sQb[4][kC][kKP];
   __shared__ float sVb[4][kC][kNC];
-  __shared__ float sgb[4][kC], sbb[4][kC];
-  // state-independent results of a chunk: decays and M (made two chunks ahead, three buffers), B (two ahead, read
-  // one ahead), Tinv (one ahead)
-  __shared__ float sgam[3][kC], sdec[3][kC], sG[kC];
-  __shared__ float sB[2][kC][kMP], sM[3][kC][kMP], sT[2][kC][kMP];
-  __shared__ __align__(16) v4f part[8][2][64];   // K S, Q S partial tiles of chunk n
-  __shared__ __align__(16) v4f part2[8][2][64];  // K K^T, Q K^T partial tiles of chunk n + 2
-  __shared__ float sB2[kC][kMP], sB4[kC][kMP], sB8[kC][kMP], sP[kC][kMP];  // the inverse's products
-  __shared__ float sDl[2][kC][kMP];
+  __shared__ __align__(16) float sgb[4][kC];
+  __shared__ float sbb[4][kC];
+  __shared__ float sTb[4][kC][kMP], sMb[4][kC][kMP];
+  __shared__ float sgam[2][kC], sdec[2][kC];    // decays of chunks n and n + 1
+  __shared__ __align__(16) v4f part[8][2][64];  // K S, Q S partial tiles
+  __shared__ float sDl[2][kC][kMP];             // Delta of the two column halves
   const int h = blockIdx.x, kh = h % HK, cg = blockIdx.y;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r = l & 15, kq = l >> 4;
   const int kb = w & 3, cb = w >> 2;
+  // Delta / O of column half 0 on wave 0, of half 1 on wave 5 (waves w and w + 4 share a SIMD), decays on wave 2
+  const bool dl_wave = w == 0 || w == 5;
   const int col = cg * kNC + cb * 16 + r;  // this lane's value column (state tile column)
   const size_t plane_sz = (size_t)H * 128 * 128;
-  const int pin = *in_plane;
+  const int pin = *in_plane, pout = pin == 0 ? 1 : 0;
   const int nch = (T + kC - 1) / kC;
   v4f S[2];
   {
@@ -123,17 +229,20 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
   }
   const int st_t = tid >> 5, st_e4 = (tid & 31) * 4, st_c = tid & 31;
   float4 pk, pq;
-  float pv, pg = 0.0f, pb = 0.0f;
+  float pv, pt, pg = 0.0f, pb = 0.0f;
   auto fetch = [&](int ch) {  // chunk ch's rows into registers (zeros, and no loads, past T)
     const int c0 = ch * kC, n = min(kC, T - c0);
     pk = make_float4(0.f, 0.f, 0.f, 0.f);
     pq = pk;
     pv = 0.0f;
+    pt = 0.0f;
     if (st_t < n) {
       pk = ld4(k + (size_t)(c0 + st_t) * stride + kh * 128 + st_e4);
       pq = ld4(q + (size_t)(c0 + st_t) * stride + kh * 128 + st_e4);
       pv = v[(size_t)(c0 + st_t) * stride + h * 128 + cg * kNC + st_c];
     }
+    if (n == kC) pt = o[((size_t)(c0 + st_t) * H + h) * 128 + cg * kNC + st_c];  // Tinv / M, parked in o
+    else if (n > 0) pt = planes[(size_t)pout * plane_sz + ((size_t)h * 128 + cg * kNC + st_c) * 128 + st_t];
     if (tid < kC) {
       pg = tid < n ? g[(size_t)(c0 + tid) * H + h] : 0.0f;
       pb = tid < n ? beta[(size_t)(c0 + tid) * H + h] : 0.0f;
@@ -143,114 +252,59 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
     *(float4*)&sKb[buf][st_t][st_e4] = pk;
     *(float4*)&sQb[buf][st_t][st_e4] = pq;
     sVb[buf][st_t][st_c] = pv;
+    if (st_c < 16) sTb[buf][st_t][st_c] = pt;
+    else sMb[buf][st_t][st_c - 16] = pt;
     if (tid < kC) {
       sgb[buf][tid] = pg;
       sbb[buf][tid] = pb;
     }
   };
-  // decays of chunk ch (wave 7): G = prefix sum of g in token order, gamma = e^G, dec = e^(G_15 - G)
+  // gamma_t = e^G_t and dec_t = e^(G_15 - G_t) of chunk ch, by one wave
   auto decays = [&](int ch) {
-    if (w == 7) {
-      const int rb = ch & 3, db = ch % 3;
-      float Gt = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kC; j++) Gt += j <= l ? sgb[rb][j] : 0.0f;
-      const float G15 = __shfl(Gt, kC - 1, 64);
-      if (l < kC) {
-        sG[l] = Gt;
-        sgam[db][l] = q27_expf(Gt);
-        sdec[db][l] = q27_expf(G15 - Gt);
-      }
+    const float Gt = prefix16(sgb[ch & 3], l);
+    const float G15 = __shfl(Gt, kC - 1, 64);
+    if (l < kC) {
+      sgam[ch & 1][l] = q27_expf(Gt);
+      sdec[ch & 1][l] = q27_expf(G15 - Gt);
     }
-  };
-  // partial K K^T and Q K^T of chunk ch over this wave's 16 keys
-  auto kk_part = [&](int ch) {
-    const int rb = ch & 3;
-    v4f kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      const int key = 16 * w + 4 * m + kq;
-      const float kr = sKb[rb][r][key];
-      kk = mfma4(kr, kr, kk);
-      qk = mfma4(sQb[rb][r][key], kr, qk);
-    }
-    part2[w][0][l] = kk;
-    part2[w][1][l] = qk;
-  };
-  // B = -A from K K^T and M from Q K^T of chunk ch (elements e0, e0 + step, ... of the 512)
-  auto reduce_bm = [&](int ch, int e0, int step) {
-    const int rb = ch & 3, pb2 = ch & 1, db = ch % 3;
-    for (int e = e0; e < 512; e += step) {
-      const int which = e >> 8, c = (e >> 4) & 15, s = e & 15;
-      const int L = 16 * (c >> 2) + s, i = c & 3;  // accumulator position of element (c, s)
-      float acc = 0.0f;
-#pragma unroll
-      for (int ww = 0; ww < 8; ww++) acc += part2[ww][which][L][i];
-      const float d = s <= c ? q27_expf(sG[c] - sG[s]) : 0.0f;
-      if (which == 0) sB[pb2][c][s] = s < c ? -((sbb[rb][c] * d) * acc) : 0.0f;
-      else sM[db][c][s] = s <= c ? d * acc : 0.0f;
-    }
-  };
-  // Tinv of chunk ch = (I + B)(I + B^2)(I + B^4)(I + B^8), by one wave
-  auto inverse = [&](int ch) {
-    const int pb2 = ch & 1;
-    put16(sB2, mm16(sB[pb2], sB[pb2], false, false, l), l);
-    wave_lds_sync();
-    put16(sB4, mm16(sB2, sB2, false, false, l), l);
-    put16(sP, mm16(sB[pb2], sB2, true, true, l), l);
-    wave_lds_sync();
-    put16(sB8, mm16(sB4, sB4, false, false, l), l);
-    put16(sB2, mm16(sP, sB4, false, true, l), l);  // (I + B)(I + B^2)(I + B^4)
-    wave_lds_sync();
-    put16(sT[pb2], mm16(sB2, sB8, false, true, l), l);
   };
 
-  // prologue: rows of chunks 0..2; decays, B, M of chunks 0 and 1; Tinv of chunk 0
   for (int c = 0; c < 3; c++) {
     fetch(c);
     stash(c);
   }
   __syncthreads();
-  for (int c = 0; c < 2 && c < nch; c++) {
-    decays(c);
-    kk_part(c);
-    __syncthreads();
-    reduce_bm(c, tid, 512);
-    __syncthreads();
-  }
-  if (w == 1) inverse(0);
+  if (w == 2) decays(0);
   __syncthreads();
 
   for (int ch = 0; ch < nch; ch++) {
     const int c0 = ch * kC, n = min(kC, T - c0);
-    const int rb = ch & 3, db = ch % 3, pb2 = ch & 1;
-    // rows of chunk ch + 3, in flight during this chunk and stored at its end (past the last chunk: no loads, zeros
-    // into a buffer no later chunk reads; unconditional, which keeps the compiler's memory-counter waits exact)
+    const int rb = ch & 3, db = ch & 1;
+    // chunk ch + 3, in flight during this chunk and stored at its end (past the last chunk: no loads, zeros into a
+    // buffer no later chunk reads; unconditional, which keeps the compiler's memory-counter waits exact)
     fetch(ch + 3);
-    // ---- X: partial K S, Q S of chunk ch; partial K K^T, Q K^T and the decays of chunk ch + 2
+    // ---- X: partial K S, Q S of chunk ch over this wave's 32 state rows
     {
       v4f ks = {0.f, 0.f, 0.f, 0.f}, qs = ks;
 #pragma unroll
       for (int b = 0; b < 2; b++) {
+        const float4 k4 = *(const float4*)&sKb[rb][r][32 * kb + 16 * b + 4 * kq];
+        const float4 q4 = *(const float4*)&sQb[rb][r][32 * kb + 16 * b + 4 * kq];
+        const float kr[4] = {k4.x, k4.y, k4.z, k4.w}, qr[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int key = 32 * kb + 16 * b + 4 * kq + i;
-          ks = mfma4(sKb[rb][r][key], S[b][i], ks);
-          qs = mfma4(sQb[rb][r][key], S[b][i], qs);
+          ks = mfma4(kr[i], S[b][i], ks);
+          qs = mfma4(qr[i], S[b][i], qs);
         }
       }
       part[w][0][l] = ks;
       part[w][1][l] = qs;
     }
-    if (ch + 2 < nch) {
-      kk_part(ch + 2);
-      decays(ch + 2);
-    }
     __syncthreads();
-    // ---- Y: waves 0 and 4 (one per column half): Delta = Tinv (beta (V - gamma K S)), O = gamma Q S + M Delta;
-    //      wave 1: Tinv of chunk ch + 1; waves 2, 3, 5, 6, 7: B and M of chunk ch + 2
-    v4f oz;  // this chunk's output tile (waves 0 and 4), stored at the end of the chunk
-    if (kb == 0) {
+    // ---- Y: Delta = Tinv (beta (V - gamma K S)) and O = gamma Q S + M Delta (one wave per column half);
+    //      the decays of chunk ch + 1
+    v4f oz;  // this chunk's output tile (the Delta waves), stored at the end of the chunk
+    if (dl_wave) {
       v4f ks = part[4 * cb][0][l], qs = part[4 * cb][1][l];
 #pragma unroll
       for (int j = 1; j < 4; j++) {
@@ -266,18 +320,16 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
       const v4f rop = tile_to_operand(rhs);
       v4f dl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int m = 0; m < 4; m++) dl = mfma4(sT[pb2][r][4 * m + kq], rop[m], dl);
-      put16(sDl[cb], dl, l);
+      for (int m = 0; m < 4; m++) dl = mfma4(sTb[rb][r][4 * m + kq], rop[m], dl);
+#pragma unroll
+      for (int i = 0; i < 4; i++) sDl[cb][4 * kq + i][r] = dl[i];
       const v4f dop = tile_to_operand(dl);
 #pragma unroll
       for (int i = 0; i < 4; i++) oz[i] = sgam[db][4 * kq + i] * qs[i];
 #pragma unroll
-      for (int m = 0; m < 4; m++) oz = mfma4(sM[db][r][4 * m + kq], dop[m], oz);
-    } else if (w == 1) {
-      if (ch + 1 < nch) inverse(ch + 1);
-    } else if (ch + 2 < nch) {
-      const int slot = (w < 4 ? w - 2 : w - 3) * 64 + l;  // 0..319 over waves 2, 3, 5, 6, 7
-      reduce_bm(ch + 2, slot, 320);
+      for (int m = 0; m < 4; m++) oz = mfma4(sMb[rb][r][4 * m + kq], dop[m], oz);
+    } else if (w == 2 && ch + 1 < nch) {
+      decays(ch + 1);
     }
     __syncthreads();
     // ---- Z: state update S <- gamma_15 S + sum_t dec_t k_t Delta_t^T; chunk ch + 3's rows to the free buffer
@@ -296,7 +348,7 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
     stash((ch + 3) & 3);
     // the output stores come after the stash: vector memory counts stores and loads together, so a store issued
     // before it would make the stash wait for the store's completion
-    if (kb == 0) {
+    if (dl_wave) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int t = 4 * kq + i;
@@ -305,7 +357,7 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
     }
     __syncthreads();
   }
-  float* dst = planes + (size_t)(pin == 0 ? 1 : 0) * plane_sz + ((size_t)h * 128 + col) * 128 + 32 * kb + 4 * kq;
+  float* dst = planes + (size_t)pout * plane_sz + ((size_t)h * 128 + col) * 128 + 32 * kb + 4 * kq;
 #pragma unroll
   for (int b = 0; b < 2; b++) st4(dst + 16 * b, S[b][0], S[b][1], S[b][2], S[b][3]);
 }
@@ -323,7 +375,12 @@ extern "C" int q27h_gdn_step_chunked(const float* q, const float* k, const float
   if (!q || !k || !v || !g || !beta || !planes || !in_plane || !o) return fail(Q27H_ERR_ARG, "gdn_step_chunked: null pointer");
   if (!aligned16(q) || !aligned16(k) || !aligned16(planes))
     return fail(Q27H_ERR_ARG, "gdn_step_chunked: q, k and planes need 16-byte alignment");
-  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(H, 128 / kNC), dim3(512), 0, stream_of(s), q, k, v, stride, g, beta, planes,
-                     in_plane, o, H, HK, T, scale);
+  if (T > 65535 * kC) return fail(Q27H_ERR_SHAPE, "gdn_step_chunked: T too large");
+  const hipStream_t st = stream_of(s);
+  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(H, (T + kC - 1) / kC), dim3(64), 0, st, q, k, stride, g, beta, planes,
+                     in_plane, o, H, HK, T);
+  if (int e = check_launch("gdn_step_chunked")) return e;
+  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(H, 128 / kNC), dim3(512), 0, st, q, k, v, stride, g, beta, planes, in_plane,
+                     o, H, HK, T, scale);
   return check_launch("gdn_step_chunked");
 }
