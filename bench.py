@@ -594,8 +594,9 @@ def bench_fused_gemv(q27, torch):
 
 def bench_gdn(q27, torch, M=2048):
     """The delta-rule recurrence (gdn_step, src/ops.cu:449-572) of one GDN layer at the model's head counts (48
-    value heads on 16 key heads, 128 x 128 f32 state each): prefill of M tokens in flip mode and a decode launch of
-    T = 4 tokens with snapshots (graph-replayed, as in a decode step). GB/s counts the compulsory bytes: state in
+    value heads on 16 key heads, 128 x 128 f32 state each): prefill of M tokens in flip mode (the chunked form on
+    matrix cores, and the sequential bit-exact kernel beside it) and a decode launch of T = 4 tokens with snapshots
+    (graph-replayed, as in a decode step). GB/s counts the compulsory bytes: state in
     and out (plus the snapshot planes), q / k per key head, v, g, beta and o per token. The recurrence is serial in
     the tokens, so its bound is the per-token latency of the update chain, not HBM; us_per_token reports that."""
     dev = torch.device("cuda:0")
@@ -622,17 +623,15 @@ def bench_gdn(q27, torch, M=2048):
         out[name] = {"us": round(us, 2), "tokens": T, "us_per_token": round(us / T, 3), "GBps": round(b / us / 1e3, 1),
                      "MB": round(b / 1e6, 2)}
         log(f"  gdn_step {name:9s} T={T:5d} {us:8.2f} us ({us / T:.3f} us/token) {b / us / 1e3:7.1f} GB/s")
-        if flip:  # the chunked form on matrix cores, same inputs
-            def fc(i=0):
-                q27.ops.gdn_step_chunked(x, x[HK * D:], x[2 * HK * D:], stride, gg, beta, planes, pin, o, H, HK, T, 0.0884)
-
-            uc = time_back_to_back(torch, fc, 20)
-            # multiply-adds of the three state products (K S, Q S, K^T Delta) per token and head, as fp32 MFMA work
-            tf = 3 * 2 * D * D * T * H / (uc * 1e-6) / 1e12
-            out[name + "_chunked"] = {"us": round(uc, 2), "tokens": T, "us_per_token": round(uc / T, 3),
-                                      "GBps": round(b / uc / 1e3, 1), "state_products_TFLOPs": round(tf, 2)}
-            log(f"  gdn_step {name + '_chunked':9s} T={T:5d} {uc:8.2f} us ({uc / T:.3f} us/token), state products "
-                f"{tf:.1f} TFLOP/s")
+        if flip:  # the same prefill on the sequential, bit-exact kernel
+            prev = q27.ops.gdn_prefill_exact(True)
+            us_seq = time_back_to_back(torch, fn, 20)
+            q27.ops.gdn_prefill_exact(prev)
+            out[name + "_sequential"] = {"us": round(us_seq, 2), "tokens": T, "us_per_token": round(us_seq / T, 3),
+                                         "GBps": round(b / us_seq / 1e3, 1)}
+            # multiply-adds of the three state products (K S, Q S, K^T Delta) per token and head, fp32 matrix cores
+            out[name]["state_products_TFLOPs"] = round(3 * 2 * D * D * T * H / (us * 1e-6) / 1e12, 2)
+            log(f"  gdn_step {name + '_sequential':9s} T={T:5d} {us_seq:8.2f} us ({us_seq / T:.3f} us/token)")
     return out
 
 

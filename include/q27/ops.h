@@ -71,6 +71,9 @@ inline void gdn_step(const float* q, const float* k, const float* v, int stride,
   q27h_check(q27h_gdn_step(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, snapshots ? 1 : 0, s,
                            flip ? 1 : 0));
 }
+// No counterpart in the reference: gdn_step's prefill sequential and bit-exact (true) or chunked on matrix cores
+// from 128 tokens on (false, the default), process-wide; returns the previous setting.
+inline bool gdn_prefill_exact(bool on) { return q27h_gdn_prefill_exact(on ? 1 : 0) != 0; }
 // src/ops.h:36
 inline void l2norm_heads(float* x, int n, int heads, int T, int stride, float eps, hipStream_t s) {
   q27h_check(q27h_l2norm_heads(x, n, heads, T, stride, eps, s));

@@ -107,10 +107,16 @@ int q27h_gdn_step(const float* q, const float* k, const float* v, int stride, co
 /* gdn_step's prefill (flip) mode in the chunked form on matrix cores: no counterpart in the reference, whose
  * prefill kernel runs token by token (src/ops.cu:449-572). Same arguments, outputs and plane semantics as
  * q27h_gdn_step with flip = 1 and snapshots = 0; the additions happen in another order, so o and the final state
- * agree with the sequential form to float32 rounding (relative 1e-5 of the largest value), not bit for bit. */
+ * agree with the sequential form to float32 rounding (relative 1e-5 of the largest value), not bit for bit.
+ * q27h_gdn_step with flip = 1 takes this path for T >= 128 unless q27h_gdn_prefill_exact(1) was called. o must not
+ * overlap the inputs (the chunks' matrices are staged in o before the outputs overwrite them). */
 int q27h_gdn_step_chunked(const float* q, const float* k, const float* v, int stride, const float* g,
                           const float* beta, float* planes, const int* in_plane, float* o, int H, int HK, int T,
                           float scale, q27h_stream_t s);
+/* Process-wide choice for gdn_step's prefill (flip) mode: 1 = always the sequential kernel (bit-exact against the
+ * CPU checker), 0 (the default) = the chunked form from 128 tokens on. Returns the previous setting. No counterpart
+ * in the reference (its prefill is sequential); for callers that need the sequential bits. */
+int q27h_gdn_prefill_exact(int on);
 /* gdn_conv_l2 (src/ops.h:112-114, src/ops.cu:731-737): gdn_conv + l2norm_heads of the first n_norm_heads heads
  * + gdn_gates in one launch. C % 128 == 0 and C / 128 - n_norm_heads == H. pf/pf_bytes ignored. */
 int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int T,

@@ -52,6 +52,7 @@ SIGNATURES = {
     "q27h_gdn_conv": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
     "q27h_gdn_step": [_p, _p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _f, _i, _p, _i],
     "q27h_gdn_step_chunked": [_p, _p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _f, _p],
+    "q27h_gdn_prefill_exact": [_i],
     "q27h_gdn_conv_l2": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _p, _p, _p, _p, _p, _p, _i, _p, _p, _sz],
     "q27h_gdn_conv_prefill": [_p, _p, _p, _p, _p, _i, _i, _i, _f, _p, _p, _p, _p, _p, _p, _i, _p],
     "q27h_gdn_flip_plane": [_p, _p],

@@ -15,6 +15,8 @@
 // 32 columns), v, e^g and beta are staged in LDS, double-buffered: the next round's global loads are in flight
 // while the current round's tokens run. The CPU checker restates this order exactly. The kernel is bound by VALU
 // issue (about 60 instructions per token and wave, two waves per SIMD), not by HBM.
+#include <atomic>
+
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
@@ -191,6 +193,14 @@ __global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __r
 
 using namespace q27h;
 
+// Prefill (flip) runs from kChunkMinT tokens on in the chunked form on matrix cores (gdn_chunk.hip), unless the
+// process asked for the sequential, bit-exact kernel. Measured (us, 48 value heads, sequential / chunked): 64 tokens
+// 18.5 / 18.5, 128 tokens 33.9 / 27.7, 512 tokens 125 / 83, 2048 tokens 489 / 294-310.
+constexpr int kChunkMinT = 128;
+static std::atomic<int> g_prefill_exact{0};
+
+extern "C" int q27h_gdn_prefill_exact(int on) { return g_prefill_exact.exchange(on ? 1 : 0); }
+
 extern "C" int q27h_gdn_step(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
                              float* planes, const int* in_plane, float* o, int H, int HK, int T, float scale, int snapshots,
                              q27h_stream_t s, int flip) {
@@ -200,6 +210,8 @@ extern "C" int q27h_gdn_step(const float* q, const float* k, const float* v, int
   if (!q || !k || !v || !g || !beta || !planes || !in_plane || !o) return fail(Q27H_ERR_ARG, "gdn_step: null pointer");
   if (!aligned16(q) || !aligned16(k) || !aligned16(planes))
     return fail(Q27H_ERR_ARG, "gdn_step: q, k and planes need 16-byte alignment");
+  if (flip && T >= kChunkMinT && !g_prefill_exact.load(std::memory_order_relaxed))
+    return q27h_gdn_step_chunked(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, s);
   if (!flip && snapshots && T > 1)
     hipLaunchKernelGGL((gdn_rec_kernel<kParts, true>), dim3(H, 128 / kCols), dim3(kCols * kParts), 0, stream_of(s), q, k,
                        v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, 0);

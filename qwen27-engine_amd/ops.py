@@ -83,6 +83,12 @@ def gdn_step_chunked(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, sc
                                       _ptr(in_plane), _ptr(o), H, HK, T, scale, _stream(s)))
 
 
+def gdn_prefill_exact(on):
+    """Process-wide: True = gdn_step's prefill always sequential (bit-exact), False = chunked from 128 tokens on.
+    Returns the previous setting."""
+    return bool(lib().q27h_gdn_prefill_exact(int(bool(on))))
+
+
 def l2norm_heads(x, n, heads, T, stride, eps, s=None):
     check(lib().q27h_l2norm_heads(_ptr(x), n, heads, T, stride, eps, _stream(s)))
 

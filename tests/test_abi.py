@@ -164,3 +164,13 @@ def test_qgemv_rejects_before_enqueue(q27):
     # fields wider than 16 bytes per chunk pad a tile's blocks to a multiple of 4 (K = 512: 2 blocks -> 4)
     assert L.q27h_qmat_bytes(12, 64, 512) == al(2 * ntb * 8 * 128) + al(ntb * 8 * 16) + al(ntb * 32)
     assert L.q27h_qmat_bytes(8, 64, 512) == 0
+
+
+def test_gdn_prefill_exact_switch(q27):
+    """The process-wide prefill choice of gdn_step is a host setting: it returns the previous value."""
+    prev = q27.ops.gdn_prefill_exact(True)
+    try:
+        assert q27.ops.gdn_prefill_exact(False) is True
+        assert q27.ops.gdn_prefill_exact(False) is False
+    finally:
+        q27.ops.gdn_prefill_exact(prev)

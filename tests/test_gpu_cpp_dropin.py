@@ -113,11 +113,13 @@ def test_gdn_prefill_layer_through_cpp_headers(q27, oracle, dl, dev, M, pin):
     err = C.create_string_buffer(512)
     p = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
     s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    prev = q27.ops.gdn_prefill_exact(True)  # the sequential recurrence, bit for bit against the checker
     rc = dl.dropin_gdn_prefill(M, p(d["conv_in"]), p(d["conv_w"]), p(d["conv_planes"]), p(plane), p(y), p(d["a"]),
                                p(d["b"]), p(d["ssm_a"]), p(d["dt_bias"]), p(g), p(beta), p(d["ssm_planes"]), p(o),
                                p(d["gnorm_w"]), p(d["z"]), p(oxq), p(oxd), p(oxs), s, err, 512)
-    assert rc == 0, err.value
     torch.cuda.synchronize()
+    q27.ops.gdn_prefill_exact(prev)
+    assert rc == 0, err.value
     oy, ocp, og, ob = oracle.gdn_conv_prefill(i["conv_in"], i["conv_w"], i["conv_planes"], pin, CC, M, 2 * KH, EPS,
                                               i["a"], i["b"], i["ssm_a"], i["dt_bias"], H)
     oo, osp = oracle.gdn_step(oy, oy[KH * D:], oy[2 * KH * D:], CC, og, ob, i["ssm_planes"], pin, H, KH, M,

@@ -1,6 +1,6 @@
-"""GPU parity of the Gated-DeltaNet recurrence (q27h_gdn_step through the C ABI) against the CPU oracle: bit-exact
-outputs and state planes for decode (T = 1..4, snapshots on / off, every input plane) and prefill (flip mode) at the
-model's head counts (48 value heads on 16 key heads, q / k / v inside one conv-output row), plus the decode ==
+"""GPU parity of the Gated-DeltaNet recurrence (q27h_gdn_step through the C ABI, sequential kernel) against the CPU
+oracle: bit-exact outputs and state planes for decode (T = 1..4, snapshots on / off, every input plane) and prefill
+(flip mode) at the model's head counts (48 value heads on 16 key heads, q / k / v inside one conv-output row), plus the decode ==
 prefill identity on the GPU and a graph replay."""
 import sys
 
@@ -18,6 +18,15 @@ SCALE = np.float32(1.0 / np.sqrt(128.0))
 def say(msg):
     print(f"[gpu-gdn] {msg}", flush=True)
     sys.stdout.flush()
+
+
+@pytest.fixture(autouse=True)
+def _sequential_prefill(q27):
+    """These tests pin the sequential kernel bit for bit; long prefills otherwise take the chunked form (checked by
+    tolerance in test_gpu_gdn_chunked.py)."""
+    prev = q27.ops.gdn_prefill_exact(True)
+    yield
+    q27.ops.gdn_prefill_exact(prev)
 
 
 def _run(q27, dev, x, stride, g, beta, planes, in_plane, H, HK, T, snapshots, flip):

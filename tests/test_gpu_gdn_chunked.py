@@ -103,3 +103,42 @@ def test_gdn_chunked_edge_values(q27, oracle, dev):
     n = H * 128 * 128
     _close(got_o, want_o, "edge o")
     _close(got_p[n:2 * n], want_p[n:2 * n], "edge state")
+
+
+def _run_step(q27, dev, x, stride, g, beta, planes, in_plane, H, HK, T):
+    import torch
+
+    dx = torch.from_numpy(x).to(dev)
+    dp = torch.from_numpy(planes).to(dev)
+    pin = torch.tensor([in_plane], dtype=torch.int32, device=dev)
+    o = torch.full((max(T, 1) * H * 128,), float("nan"), device=dev)
+    q27.ops.gdn_step(dx, dx[HK * 128:], dx[2 * HK * 128:], stride, torch.from_numpy(g).to(dev),
+                     torch.from_numpy(beta).to(dev), dp, pin, o, H, HK, T, float(SCALE), False, flip=True)
+    torch.cuda.synchronize()
+    return o.cpu().numpy()[: T * H * 128], dp.cpu().numpy()
+
+
+def test_gdn_step_prefill_dispatch(q27, oracle, dev):
+    """gdn_step with flip: from 128 tokens on the chunked form (same bits as q27h_gdn_step_chunked), below it and in
+    exact mode the sequential kernel (the checker's bits)."""
+    H, HK = cd.HV, cd.KH
+    prev = q27.ops.gdn_prefill_exact(False)
+    try:
+        for M in (2048, 128):
+            say(f"gdn_step prefill dispatch M={M}")
+            x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(500 + M), M)
+            got_o, got_p = _run_step(q27, dev, x, stride, g, beta, planes, 0, H, HK, M)
+            ch_o, ch_p = _run(q27, dev, x, stride, g, beta, planes, 0, H, HK, M)
+            assert np.array_equal(got_o.view(np.uint32), ch_o.view(np.uint32)), M
+            assert np.array_equal(got_p.view(np.uint32), ch_p.view(np.uint32)), M
+        for M, exact in ((127, False), (300, True)):
+            say(f"gdn_step prefill sequential M={M} exact={exact}")
+            q27.ops.gdn_prefill_exact(exact)
+            x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(600 + M), M)
+            got_o, got_p = _run_step(q27, dev, x, stride, g, beta, planes, 1, H, HK, M)
+            want_o, want_p = oracle.gdn_step(x, x[HK * 128:], x[2 * HK * 128:], stride, g, beta, planes, 1, H, HK, M,
+                                             SCALE, False, True)
+            assert np.array_equal(got_o.view(np.uint32), want_o.view(np.uint32)), M
+            assert np.array_equal(got_p.view(np.uint32), want_p.view(np.uint32)), M
+    finally:
+        q27.ops.gdn_prefill_exact(prev)
