@@ -12,7 +12,7 @@
 // which unrolls the per-token rule  delta = (v - e^g S^T k) beta,  S <- e^g S + k delta^T,  o = scale S^T q  over the
 // chunk (the sequential kernel's comment gives the per-token form).
 //
-// Two launches. gdn_chunk_prep_kernel (one wave per value head and chunk, all chunks in parallel) forms Tinv and M,
+// Two launches. gdn_chunk_prep_kernel (one wave per key head and chunk, all chunks in parallel) forms Tinv and M,
 // which do not depend on the state, and parks them where the second launch finds them: for a full chunk in the
 // chunk's own rows of o (one 16 x 32 copy per 32-column group of the head, [t][j] = Tinv[t][j] for j < 16, M[t][j - 16]
 // otherwise), which the recurrence overwrites only with that group's own outputs after reading them; for a last,
@@ -130,6 +130,8 @@ __device__ __forceinline__ v4f unit_lower_inverse(const float (*B)[kMP], int r, 
 }
 
 // ---------------------------------------------------------------- prep: Tinv and M of every chunk
+// One wave per (key head, chunk): K K^T and Q K^T once, then Tinv and M of every value head on that key head (their
+// g and beta differ).
 __global__ void __launch_bounds__(64) gdn_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                             int stride, const float* __restrict__ g,
                                                             const float* __restrict__ beta, float* __restrict__ planes,
@@ -140,7 +142,7 @@ __global__ void __launch_bounds__(64) gdn_chunk_prep_kernel(const float* __restr
   __shared__ __align__(16) float sg[kC];
   __shared__ float sb[kC];
   __shared__ float sB[kC][kMP];
-  const int h = blockIdx.x, c = blockIdx.y, kh = h % HK;
+  const int kh = blockIdx.x, c = blockIdx.y;
   const int c0 = c * kC, n = min(kC, T - c0);
   const int l = threadIdx.x, r = l & 15, kq = l >> 4;
 #pragma unroll
@@ -154,42 +156,46 @@ __global__ void __launch_bounds__(64) gdn_chunk_prep_kernel(const float* __restr
     *(float4*)&sK[t][e4] = kv4;
     *(float4*)&sQ[t][e4] = qv4;
   }
-  if (l < kC) {
-    sg[l] = l < n ? g[(size_t)(c0 + l) * H + h] : 0.0f;
-    sb[l] = l < n ? beta[(size_t)(c0 + l) * H + h] : 0.0f;
-  }
   __syncthreads();
   const v4f kk = gram16(sK, sK, r, kq), qk = gram16(sQ, sK, r, kq);
-  const float Gt = prefix16(sg, l);
-  const float Gs = __shfl(Gt, r, 64);
-  v4f mt;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int cc = 4 * kq + i;
-    const float Gc = __shfl(Gt, cc, 64);  // every lane takes part (a lane exchange reads from active lanes only)
-    const float d = r <= cc ? q27_expf(Gc - Gs) : 0.0f;
-    sB[cc][r] = r < cc ? -((sb[cc] * d) * kk[i]) : 0.0f;
-    mt[i] = r <= cc ? d * qk[i] : 0.0f;
-  }
-  __syncthreads();
-  const v4f ti = unit_lower_inverse(sB, r, kq);
   const size_t plane_sz = (size_t)H * 128 * 128;
   const int pout = *in_plane == 0 ? 1 : 0;
-#pragma unroll
-  for (int cg = 0; cg < 128 / kNC; cg++) {
+  for (int h = kh; h < H; h += HK) {
+    if (l < kC) {
+      sg[l] = l < n ? g[(size_t)(c0 + l) * H + h] : 0.0f;
+      sb[l] = l < n ? beta[(size_t)(c0 + l) * H + h] : 0.0f;
+    }
+    __syncthreads();
+    const float Gt = prefix16(sg, l);
+    const float Gs = __shfl(Gt, r, 64);
+    v4f mt;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int t = 4 * kq + i;
-      if (n == kC) {
-        float* dst = o + ((size_t)(c0 + t) * H + h) * 128 + kNC * cg;
-        dst[r] = ti[i];
-        dst[16 + r] = mt[i];
-      } else {
-        float* dst = planes + (size_t)pout * plane_sz + ((size_t)h * 128 + kNC * cg) * 128 + t;
-        dst[(size_t)r * 128] = ti[i];
-        dst[(size_t)(16 + r) * 128] = mt[i];
+      const int cc = 4 * kq + i;
+      const float Gc = __shfl(Gt, cc, 64);  // every lane takes part (a lane exchange reads from active lanes only)
+      const float d = r <= cc ? q27_expf(Gc - Gs) : 0.0f;
+      sB[cc][r] = r < cc ? -((sb[cc] * d) * kk[i]) : 0.0f;
+      mt[i] = r <= cc ? d * qk[i] : 0.0f;
+    }
+    __syncthreads();
+    const v4f ti = unit_lower_inverse(sB, r, kq);
+#pragma unroll
+    for (int cg = 0; cg < 128 / kNC; cg++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = 4 * kq + i;
+        if (n == kC) {
+          float* dst = o + ((size_t)(c0 + t) * H + h) * 128 + kNC * cg;
+          dst[r] = ti[i];
+          dst[16 + r] = mt[i];
+        } else {
+          float* dst = planes + (size_t)pout * plane_sz + ((size_t)h * 128 + kNC * cg) * 128 + t;
+          dst[(size_t)r * 128] = ti[i];
+          dst[(size_t)(16 + r) * 128] = mt[i];
+        }
       }
     }
+    __syncthreads();  // sg, sb and sB are refilled for the next value head
   }
 }
 
@@ -377,8 +383,8 @@ extern "C" int q27h_gdn_step_chunked(const float* q, const float* k, const float
     return fail(Q27H_ERR_ARG, "gdn_step_chunked: q, k and planes need 16-byte alignment");
   if (T > 65535 * kC) return fail(Q27H_ERR_SHAPE, "gdn_step_chunked: T too large");
   const hipStream_t st = stream_of(s);
-  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(H, (T + kC - 1) / kC), dim3(64), 0, st, q, k, stride, g, beta, planes,
-                     in_plane, o, H, HK, T);
+  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(min(H, HK), (T + kC - 1) / kC), dim3(64), 0, st, q, k, stride, g, beta,
+                     planes, in_plane, o, H, HK, T);
   if (int e = check_launch("gdn_step_chunked")) return e;
   hipLaunchKernelGGL(gdn_chunk_kernel, dim3(H, 128 / kNC), dim3(512), 0, st, q, k, v, stride, g, beta, planes, in_plane,
                      o, H, HK, T, scale);
