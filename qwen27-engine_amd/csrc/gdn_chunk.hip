@@ -23,7 +23,7 @@
 // a column half (their operand steps read keys in the state tile's own row order, so the state never leaves its
 // accumulators); Delta and O are formed by one wave per column half, with the 16 x 16 right-hand side turned into
 // MFMA operands by lane swaps; the update is an MFMA into the state tiles. A chunk's rows (k, q, v, g, beta, Tinv, M)
-// are loaded three chunks ahead into one of four LDS buffers.
+// are loaded kNB - 1 = three chunks ahead into one of four LDS buffers.
 #include "q27h_device.h"
 #include "q27h_internal.h"
 
@@ -35,6 +35,9 @@ constexpr int kC = 16;     // tokens per chunk
 constexpr int kNC = 32;    // value columns per workgroup of the recurrence
 constexpr int kKP = 132;   // padded LDS row of a chunk's k / q (floats)
 constexpr int kMP = 17;    // padded LDS row of the 16 x 16 matrices
+// row buffers of the recurrence: rows are loaded kNB - 1 chunks ahead (3, 4 or 5 buffers measured the same:
+// 282-290 us per 2048-token layer)
+constexpr int kNB = 4;
 
 __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -205,13 +208,13 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
                                                         const float* __restrict__ g, const float* __restrict__ beta,
                                                         float* __restrict__ planes, const int* __restrict__ in_plane,
                                                         float* __restrict__ o, int H, int HK, int T, float scale) {
-  // a chunk's rows, four buffers (chunk n in use, n + 1 and n + 2 waiting, n + 3 arriving)
-  __shared__ __align__(16) float sKb[4][kC][kKP];
-  __shared__ __align__(16) float sQb[4][kC][kKP];
-  __shared__ float sVb[4][kC][kNC];
-  __shared__ __align__(16) float sgb[4][kC];
-  __shared__ float sbb[4][kC];
-  __shared__ float sTb[4][kC][kMP], sMb[4][kC][kMP];
+  // a chunk's rows, kNB buffers (chunk n in use, the next ones waiting, n + kNB - 1 arriving)
+  __shared__ __align__(16) float sKb[kNB][kC][kKP];
+  __shared__ __align__(16) float sQb[kNB][kC][kKP];
+  __shared__ float sVb[kNB][kC][kNC];
+  __shared__ __align__(16) float sgb[kNB][kC];
+  __shared__ float sbb[kNB][kC];
+  __shared__ float sTb[kNB][kC][kMP], sMb[kNB][kC][kMP];
   __shared__ float sgam[2][kC], sdec[2][kC];    // decays of chunks n and n + 1
   __shared__ __align__(16) v4f part[8][2][64];  // K S, Q S partial tiles
   __shared__ float sDl[2][kC][kMP];             // Delta of the two column halves
@@ -267,7 +270,7 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
   };
   // gamma_t = e^G_t and dec_t = e^(G_15 - G_t) of chunk ch, by one wave
   auto decays = [&](int ch) {
-    const float Gt = prefix16(sgb[ch & 3], l);
+    const float Gt = prefix16(sgb[ch % kNB], l);
     const float G15 = __shfl(Gt, kC - 1, 64);
     if (l < kC) {
       sgam[ch & 1][l] = q27_expf(Gt);
@@ -275,7 +278,7 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
     }
   };
 
-  for (int c = 0; c < 3; c++) {
+  for (int c = 0; c < kNB - 1; c++) {
     fetch(c);
     stash(c);
   }
@@ -285,10 +288,10 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
 
   for (int ch = 0; ch < nch; ch++) {
     const int c0 = ch * kC, n = min(kC, T - c0);
-    const int rb = ch & 3, db = ch & 1;
-    // chunk ch + 3, in flight during this chunk and stored at its end (past the last chunk: no loads, zeros into a
+    const int rb = ch % kNB, db = ch & 1;
+    // chunk ch + kNB - 1, in flight during this chunk and stored at its end (past the last chunk: no loads, zeros into a
     // buffer no later chunk reads; unconditional, which keeps the compiler's memory-counter waits exact)
-    fetch(ch + 3);
+    fetch(ch + kNB - 1);
     // ---- X: partial K S, Q S of chunk ch over this wave's 32 state rows
     {
       v4f ks = {0.f, 0.f, 0.f, 0.f}, qs = ks;
@@ -338,7 +341,7 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
       decays(ch + 1);
     }
     __syncthreads();
-    // ---- Z: state update S <- gamma_15 S + sum_t dec_t k_t Delta_t^T; chunk ch + 3's rows to the free buffer
+    // ---- Z: state update S <- gamma_15 S + sum_t dec_t k_t Delta_t^T; chunk ch + kNB - 1's rows to the free buffer
     {
       const float g15 = sgam[db][kC - 1];
 #pragma unroll
@@ -351,7 +354,7 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
         }
       }
     }
-    stash((ch + 3) & 3);
+    stash((ch + kNB - 1) % kNB);
     // the output stores come after the stash: vector memory counts stores and loads together, so a store issued
     // before it would make the stash wait for the store's completion
     if (dl_wave) {
