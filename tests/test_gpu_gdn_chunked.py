@@ -142,3 +142,36 @@ def test_gdn_step_prefill_dispatch(q27, oracle, dev):
             assert np.array_equal(got_p.view(np.uint32), want_p.view(np.uint32)), M
     finally:
         q27.ops.gdn_prefill_exact(prev)
+
+
+def test_gdn_chunked_replays_in_hip_graph(q27, dev):
+    """The chunked prefill (two launches, Tinv / M staged in o) captured in a HIP graph: every replay gives the eager
+    launch's bits (no allocation, no host synchronisation, nothing left over from the previous replay)."""
+    import torch
+
+    H, HK, M = cd.HV, cd.KH, 300
+    say(f"gdn chunked graph replay M={M}")
+    x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(700), M)
+    want_o, want_p = _run(q27, dev, x, stride, g, beta, planes, 1, H, HK, M)
+    dx, dg, db = (torch.from_numpy(a).to(dev) for a in (x, g, beta))
+    p0 = torch.from_numpy(planes).to(dev)
+    dp = p0.clone()
+    pin = torch.ones(1, dtype=torch.int32, device=dev)
+    o = torch.zeros(M * H * 128, device=dev)
+    s = torch.cuda.Stream()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        q27.ops.gdn_step_chunked(dx, dx[HK * 128:], dx[2 * HK * 128:], stride, dg, db, dp, pin, o, H, HK, M,
+                                 float(SCALE))
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr, stream=s):
+            q27.ops.gdn_step_chunked(dx, dx[HK * 128:], dx[2 * HK * 128:], stride, dg, db, dp, pin, o, H, HK, M,
+                                     float(SCALE))
+    for _ in range(3):
+        dp.copy_(p0)
+        o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(o.cpu().numpy().view(np.uint32), want_o.view(np.uint32)), "graph replay o"
+        assert np.array_equal(dp.cpu().numpy().view(np.uint32), want_p.view(np.uint32)), "graph replay planes"
