@@ -371,7 +371,8 @@ int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* 
   // fast path (two A/B runs on one box; the row kernel's waves otherwise often wait on a fallback block). A
   // 1024-thread form with 5 values per lane, the reference's layout, measured slower: 4.0 against 3.3 us per decode
   // node. A persistent form (a grid of 1-4 workgroups per CU, each walking rows with the next row's loads in flight)
-  // measured slower at 2048 rows: 30.0-31.7 against 27.6 us for sum_norm_rows.
+  // measured slower at 2048 rows: 30.0-31.7 against 27.6 us for sum_norm_rows. Fewer resident workgroups per CU
+  // (dynamic LDS of 32, 40 or 54 KB per workgroup) made no difference to the pass; 80 KB made it 8% slower.
   hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
                      xq, xd, xs, wown, wrecv, qb_shift);
   return check_launch(fn);
