@@ -685,6 +685,37 @@ def bench_upload(q27, torch, gib=1.0):
     return out
 
 
+def bench_repack(q27, torch, N=17408, K=5120):
+    """The repack of qmat_upload (src/qmat.h:34-36) for each weight type at 17408 x 5120: raw GGUF rows already in
+    HBM (random bytes: the repack only moves bytes), two raw copies alternated so the MALL does not serve the input;
+    mean of 10 launches. GB/s of raw bytes read + repacked bytes written."""
+    dev = torch.device("cuda:0")
+    out = {}
+    for name, (tid, bb, _) in GEMV_TYPES.items():
+        raw_bytes = N * K // 256 * bb
+        nbytes = q27.ops.qmat_bytes(tid, N, K)
+        raws = [torch.randint(0, 256, (raw_bytes,), dtype=torch.uint8, device=dev) for _ in range(2)]
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        st = torch.cuda.current_stream().cuda_stream
+        L = q27.ops.lib()
+        for i in range(2):
+            q27.ops.check(L.q27h_qmat_repack(tid, N, K, raws[i].data_ptr(), buf.data_ptr(), st))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 10
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(n):
+            q27.ops.check(L.q27h_qmat_repack(tid, N, K, raws[i % 2].data_ptr(), buf.data_ptr(), st))
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        out[name] = {"us": round(us, 2), "raw_MB": round(raw_bytes / 1e6, 1),
+                     "GBps": round((raw_bytes + nbytes) / us / 1e3, 1)}
+        log(f"  repack {name:8s} {N} x {K}: {us:8.2f} us, {(raw_bytes + nbytes) / us / 1e3:7.1f} GB/s")
+        del raws, buf
+    return out
+
+
 def bench_wire(q27, torch, M=2048):
     """The two-card wire formats at the prefill batch (src/prefill.cu:338-406) on one GPU: to_q8_wire with carried
     error feedback, add_norm_rows_q8 (h = null, xs) and to_bf16 of [M][5120], both q8 widths. Three buffer sets
@@ -886,6 +917,7 @@ def main():
                     help="prefill step inputs: cold = every layer reads its own (default), warm = one set reused by all layers")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
+    ap.add_argument("--repack-only", action="store_true", help="only the qmat_upload repack of each weight type")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the fused-op path has no multi-GPU form in this build "
@@ -901,6 +933,9 @@ def main():
     q27.lib()
     torch.cuda.init()
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.repack_only:
+        print(json.dumps({"qmat_repack": bench_repack(q27, torch)}), flush=True)
+        return
 
     # ---- prefill pass (the step)
     P = Pass(q27, torch, 2048, decode=False, cold=args.buffers == "cold")
@@ -1044,6 +1079,7 @@ def main():
     fused_gemv = bench_fused_gemv(q27, torch)
     gdn_rec = bench_gdn(q27, torch)
     upload = bench_upload(q27, torch)
+    repack = bench_repack(q27, torch)
 
     if args.calib_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -1099,6 +1135,7 @@ def main():
         "decode_quantize_gemv_fused": fused_gemv,
         "gdn_recurrence": gdn_rec,
         "gguf_upload": upload,
+        "qmat_repack": repack,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -99,150 +99,266 @@ size_t layout(int type, int N, int K, size_t off[5]) {
   return o + align256(ntiles * nb * F.dw);
 }
 
-// ---------------------------------------------------------------- repack (one thread per chunk)
-template <int TYPE>
-__global__ void repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ f0, uint8_t* __restrict__ f1,
-                              uint8_t* __restrict__ f2, uint8_t* __restrict__ f3, uint8_t* __restrict__ dd, int nb,
-                              size_t nchunks) {
-  const size_t chunk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (chunk >= nchunks) return;
-  constexpr Fmt F = fmt_of(TYPE);
-  const int s = (int)(chunk & 7);
-  const size_t tb = chunk >> 3;
-  const int b = (int)(tb % nb);
-  const size_t tile = tb / nb;
-  // the chunk's records (8 rows each), then scattered to the field layout
-  uint8_t o0[F.w[0]], o1[F.w[1] ? F.w[1] : 1], o2[F.w[2] ? F.w[2] : 1], o3[F.w[3] ? F.w[3] : 1];
-  uint32_t nib = 0;
-  for (int r = 0; r < 8; r++) {
-    const uint8_t* src = raw + ((tile * 8 + r) * nb + b) * F.bb;
-    uint8_t* od = dd + tb * F.dw;
-    if constexpr (TYPE == kQ4K) {  // d, dmin, scales[12], qs[128]
-      const uint8_t* qs = src + 16 + 32 * (s / 2);
-      const int sh = 4 * (s & 1);
-      for (int k = 0; k < 16; k++)  // byte k: weight k (low nibble), weight k + 16 (high nibble)
-        o0[16 * r + k] = (uint8_t)(((qs[k] >> sh) & 0xF) | (((qs[k + 16] >> sh) & 0xF) << 4));
-      const uint8_t* sc = src + 4;
-      int scv, mv;
-      if (s < 4) {
-        scv = sc[s] & 63;
-        mv = sc[s + 4] & 63;
-      } else {
-        scv = (sc[s + 4] & 0xF) | ((sc[s - 4] >> 6) << 4);
-        mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
-      }
-      o1[2 * r] = (uint8_t)scv;
-      o1[2 * r + 1] = (uint8_t)mv;
-      if (s == 0)
-        for (int k = 0; k < 4; k++) od[4 * r + k] = src[k];
-    } else if constexpr (TYPE == kQ6K) {  // ql[128], qh[64], scales[16], d
-      const int n = s / 4, j = s % 4;
-      uint8_t q[32];
-      for (int l = 0; l < 32; l++) {
-        const uint8_t lo = src[64 * n + 32 * (j & 1) + l];
-        const uint8_t hi = src[128 + 32 * n + l];
-        q[l] = (uint8_t)(((j < 2 ? lo : lo >> 4) & 0xF) | (((hi >> (2 * j)) & 3) << 4));
-      }
-      for (int k = 0; k < 16; k++) o0[16 * r + k] = (uint8_t)((q[k] & 0xF) | ((q[k + 16] & 0xF) << 4));
-      for (int h = 0; h < 2; h++)  // word h (weights 16 h ..): byte k holds the high bits of weights 16 h + k + 4 i
-        for (int k = 0; k < 4; k++) {
-          uint8_t v = 0;
-          for (int i = 0; i < 4; i++) v |= (uint8_t)(((q[16 * h + k + 4 * i] >> 4) & 3) << (2 * i));
-          o1[8 * r + 4 * h + k] = v;
-        }
-      o2[2 * r] = src[192 + 8 * n + 2 * j];
-      o2[2 * r + 1] = src[192 + 8 * n + 2 * j + 1];
-      if (s == 0) {
-        od[2 * r] = src[208];
-        od[2 * r + 1] = src[209];
-      }
-    } else if constexpr (TYPE == kIQ3S) {  // d, qs[64], qh[8], signs[32], scales[4]
-      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
-      for (int k = 0; k < 4; k++) o1[4 * r + k] = src[74 + 4 * s + k];
-      o2[r] = src[66 + s];
-      nib |= (uint32_t)((src[106 + s / 2] >> (4 * (s & 1))) & 0xF) << (4 * r);
-      if (s == 0) {
-        od[2 * r] = src[0];
-        od[2 * r + 1] = src[1];
-      }
-    } else if constexpr (TYPE == kIQ4XS) {  // d, scales_h (u16), scales_l[4], qs[128]
-      for (int k = 0; k < 16; k++) o0[16 * r + k] = src[8 + 16 * s + k];
-      const int sh = src[2] | (src[3] << 8);
-      const int l = ((src[4 + s / 2] >> (4 * (s & 1))) & 0xF) | (((sh >> (2 * s)) & 3) << 4);
-      o1[r] = (uint8_t)(int8_t)(l - 32);
-      if (s == 0) {
-        od[2 * r] = src[0];
-        od[2 * r + 1] = src[1];
-      }
-    } else if constexpr (TYPE == kQ2K) {  // scales[16], qs[64], d, dmin
-      // sub-block s = 4 n + j: weights 128 n + 32 j + l = (qs[32 n + l] >> 2 j) & 3. Word h (weights 16 h ..):
-      // byte k holds weights 16 h + k + 4 i at bits 2 i.
-      const int n = s / 4, j = s % 4;
-      const uint8_t* qs = src + 16 + 32 * n;
-      for (int h = 0; h < 2; h++)
-        for (int k = 0; k < 4; k++) {
-          uint8_t v = 0;
-          for (int i = 0; i < 4; i++) v |= (uint8_t)(((qs[16 * h + k + 4 * i] >> (2 * j)) & 3) << (2 * i));
-          o0[8 * r + 4 * h + k] = v;
-        }
-      o1[2 * r] = src[8 * n + 2 * j];
-      o1[2 * r + 1] = src[8 * n + 2 * j + 1];
-      if (s == 0)
-        for (int k = 0; k < 4; k++) od[4 * r + k] = src[80 + k];
-    } else if constexpr (TYPE == kIQ2XXS) {  // d, per sub-block 4 grid indices + a sign / scale word
-      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
-      if (s == 0) {
-        od[2 * r] = src[0];
-        od[2 * r + 1] = src[1];
-      }
-    } else if constexpr (TYPE == kIQ2XS) {  // d, qs[32] (u16 index + signs), scales[8]
-      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
-      o1[r] = src[66 + s];
-      if (s == 0) {
-        od[2 * r] = src[0];
-        od[2 * r + 1] = src[1];
-      }
-    } else if constexpr (TYPE == kIQ3XXS) {  // d, qs[64], scales_and_signs[32]
-      for (int k = 0; k < 8; k++) o0[8 * r + k] = src[2 + 8 * s + k];
-      for (int k = 0; k < 4; k++) o1[4 * r + k] = src[66 + 4 * s + k];
-      if (s == 0) {
-        od[2 * r] = src[0];
-        od[2 * r + 1] = src[1];
-      }
-    } else if constexpr (TYPE == kIQ2S) {  // d, qs[32], signs[32], qh[8], scales[8]
-      for (int k = 0; k < 4; k++) o0[4 * r + k] = src[2 + 4 * s + k];
-      for (int k = 0; k < 4; k++) o1[4 * r + k] = src[34 + 4 * s + k];
-      o2[r] = src[66 + s];
-      o3[r] = src[74 + s];
-      if (s == 0) {
-        od[2 * r] = src[0];
-        od[2 * r + 1] = src[1];
-      }
-    } else if constexpr (TYPE == kIQ1M) {  // qs[32], qh[16], scales[8] (4 x u16, fp16 scale in the top nibbles)
-      for (int k = 0; k < 4; k++) o0[4 * r + k] = src[4 * s + k];
-      o1[2 * r] = src[32 + 2 * s];
-      o1[2 * r + 1] = src[33 + 2 * s];
-      uint16_t s16[4];
-      for (int k = 0; k < 4; k++) s16[k] = (uint16_t)(src[48 + 2 * k] | (src[49 + 2 * k] << 8));
-      o2[r] = (uint8_t)((s16[s / 2] >> (6 * (s % 2))) & 63);
-      if (s == 0) {
-        const uint16_t dh = (uint16_t)((s16[0] >> 12) | ((s16[1] >> 8) & 0x00F0) | ((s16[2] >> 4) & 0x0F00) | (s16[3] & 0xF000));
-        od[2 * r] = (uint8_t)(dh & 0xFF);
-        od[2 * r + 1] = (uint8_t)(dh >> 8);
-      }
-    }
+// ---------------------------------------------------------------- repack (one workgroup per tile and group of 4 blocks)
+// The 8 rows x (up to) 4 GGUF blocks of a group are read into LDS with coalesced 4-byte loads; thread t = 8 c + r
+// (chunk c = 8 bl + s of the group, row r) builds row r's part of chunk c's record (every field of a chunk record is
+// row-major: W = wf / 8 bytes per row) into an LDS image of the destination, which is then written with 16-byte
+// stores. A group covers exactly the 32 chunks of one group of the wide (16-byte piece) fields, so its image of such a
+// field is one contiguous 32 x wf-byte range; the narrow fields and the scales of the group's blocks are contiguous
+// too. Chunks of a tail group past the row's last block are padding of the wide fields and are written as zeros.
+constexpr int kRepackBlocks = 4;
+
+// Writes the W bytes v (row r of chunk c) to their place in the group image of a field of wf bytes per chunk.
+template <int WF, int W>
+__device__ __forceinline__ void put_row(uint8_t* img, int c, int r, const uint8_t (&v)[W], uint32_t keep) {
+  const int j0 = W * r;
+  uint8_t* d = img + (WF <= 16 ? c * WF + j0 : (j0 / 16) * 512 + c * 16 + j0 % 16);
+  if constexpr (W % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < W / 4; k++)
+      ((uint32_t*)d)[k] = ((uint32_t)v[4 * k] | ((uint32_t)v[4 * k + 1] << 8) | ((uint32_t)v[4 * k + 2] << 16) |
+                           ((uint32_t)v[4 * k + 3] << 24)) & keep;
+  } else if constexpr (W == 2) {
+    *(uint16_t*)d = (uint16_t)(((uint32_t)v[0] | ((uint32_t)v[1] << 8)) & keep);
+  } else {
+    *d = (uint8_t)(v[0] & keep);
   }
-  auto put = [&](uint8_t* f, int wf, const uint8_t* rec) {
-    uint8_t* dst = f + field_off(wf, tile, nb, b, s);
-    for (int k = 0; k < wf; k++) dst[(wf <= 16 ? 0 : (k / 16) * 512) + (wf <= 16 ? k : k % 16)] = rec[k];
-  };
-  put(f0, F.w[0], o0);
-  if constexpr (F.nf > 1) put(f1, F.w[1], o1);
-  if constexpr (F.nf > 2) put(f2, F.w[2], o2);
-  if constexpr (TYPE == kIQ3S) *(uint32_t*)(f3 + field_off(4, tile, nb, b, s)) = nib;
-  else if constexpr (F.nf > 3) put(f3, F.w[3], o3);
 }
 
+// Copies n bytes (a multiple of 16) of an LDS image to dst (16-byte aligned).
+__device__ __forceinline__ void copy_out(uint8_t* __restrict__ dst, const uint8_t* img, int n) {
+  for (int u = threadIdx.x; u < n / 16; u += 256) ((uint4*)dst)[u] = ((const uint4*)img)[u];
+}
+
+template <int TYPE>
+__global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ f0,
+                                                     uint8_t* __restrict__ f1, uint8_t* __restrict__ f2,
+                                                     uint8_t* __restrict__ f3, uint8_t* __restrict__ dd, int nb) {
+  constexpr Fmt F = fmt_of(TYPE);
+  constexpr int RS = kRepackBlocks * F.bb;  // LDS bytes per row
+  __shared__ __align__(16) uint8_t sraw[8 * RS];
+  __shared__ __align__(16) uint8_t img0[32 * F.w[0]];
+  __shared__ __align__(16) uint8_t img1[32 * (F.w[1] ? F.w[1] : 16)];
+  __shared__ __align__(16) uint8_t img2[32 * (F.w[2] ? F.w[2] : 16)];
+  __shared__ __align__(16) uint8_t img3[32 * (F.w[3] ? F.w[3] : 16)];
+  __shared__ __align__(16) uint8_t imgd[kRepackBlocks * F.dw];
+  const int ngroups = (nb + kRepackBlocks - 1) / kRepackBlocks;
+  const size_t tile = blockIdx.x / ngroups;
+  const int g = (int)(blockIdx.x % ngroups);
+  const int b0 = g * kRepackBlocks;
+  const int nbg = min(kRepackBlocks, nb - b0);
+  const int t = threadIdx.x;
+
+  // raw rows of the group -> LDS (row r at r * RS): 32 lanes per row, 4-byte loads when every row starts at a
+  // multiple of 4 bytes (the group's start in its row, 4 g blocks, always does), else 2-byte loads (GGUF blocks have
+  // even sizes), or bytes for an odd raw pointer
+  const int L = nbg * F.bb;
+  {
+    const int rr = t >> 5, k0 = t & 31;
+    const uint8_t* row = raw + ((tile * 8 + rr) * nb + b0) * F.bb;
+    uint8_t* lrow = sraw + rr * RS;
+    if ((((uintptr_t)raw | ((size_t)nb * F.bb)) & 3) == 0) {
+      for (int k = k0; k < L / 4; k += 32)
+        ((uint32_t*)lrow)[k] = __builtin_nontemporal_load((const uint32_t*)row + k);
+      if ((L & 2) && k0 == 0) ((uint16_t*)lrow)[L / 2 - 1] = __builtin_nontemporal_load((const uint16_t*)row + L / 2 - 1);
+    } else if (((uintptr_t)raw & 1) == 0) {
+      for (int k = k0; k < L / 2; k += 32)
+        ((uint16_t*)lrow)[k] = __builtin_nontemporal_load((const uint16_t*)row + k);
+    } else {
+      for (int k = k0; k < L; k += 32) lrow[k] = row[k];
+    }
+  }
+  __syncthreads();
+
+  const int c = t >> 3, r = t & 7, bl = c >> 3, s = c & 7;
+  const uint32_t keep = bl < nbg ? ~0u : 0u;
+  const uint8_t* src = sraw + r * RS + (bl < nbg ? bl : 0) * F.bb;
+  uint8_t* od = imgd + bl * F.dw;
+  const bool put_d = s == 0 && bl < nbg;
+  if constexpr (TYPE == kQ4K) {  // d, dmin, scales[12], qs[128]
+    const uint8_t* qs = src + 16 + 32 * (s / 2);
+    const int sh = 4 * (s & 1);
+    uint8_t o0[16], o1[2];
+#pragma unroll
+    for (int k = 0; k < 16; k++)  // byte k: weight k (low nibble), weight k + 16 (high nibble)
+      o0[k] = (uint8_t)(((qs[k] >> sh) & 0xF) | (((qs[k + 16] >> sh) & 0xF) << 4));
+    const uint8_t* sc = src + 4;
+    int scv, mv;
+    if (s < 4) {
+      scv = sc[s] & 63;
+      mv = sc[s + 4] & 63;
+    } else {
+      scv = (sc[s + 4] & 0xF) | ((sc[s - 4] >> 6) << 4);
+      mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
+    }
+    o1[0] = (uint8_t)scv;
+    o1[1] = (uint8_t)mv;
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    if (put_d)
+      for (int k = 0; k < 4; k++) od[4 * r + k] = src[k];
+  } else if constexpr (TYPE == kQ6K) {  // ql[128], qh[64], scales[16], d
+    const int n = s / 4, j = s % 4;
+    uint8_t q[32], o0[16], o1[8], o2[2];
+#pragma unroll
+    for (int l = 0; l < 32; l++) {
+      const uint8_t lo = src[64 * n + 32 * (j & 1) + l];
+      const uint8_t hi = src[128 + 32 * n + l];
+      q[l] = (uint8_t)(((j < 2 ? lo : lo >> 4) & 0xF) | (((hi >> (2 * j)) & 3) << 4));
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) o0[k] = (uint8_t)((q[k] & 0xF) | ((q[k + 16] & 0xF) << 4));
+#pragma unroll
+    for (int h = 0; h < 2; h++)  // word h (weights 16 h ..): byte k holds the high bits of weights 16 h + k + 4 i
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint8_t v = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) v |= (uint8_t)(((q[16 * h + k + 4 * i] >> 4) & 3) << (2 * i));
+        o1[4 * h + k] = v;
+      }
+    o2[0] = src[192 + 8 * n + 2 * j];
+    o2[1] = src[192 + 8 * n + 2 * j + 1];
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    put_row<F.w[2]>(img2, c, r, o2, keep);
+    if (put_d) {
+      od[2 * r] = src[208];
+      od[2 * r + 1] = src[209];
+    }
+  } else if constexpr (TYPE == kIQ3S) {  // d, qs[64], qh[8], signs[32], scales[4]
+    uint8_t o0[8], o1[4], o2[1];
+#pragma unroll
+    for (int k = 0; k < 8; k++) o0[k] = src[2 + 8 * s + k];
+#pragma unroll
+    for (int k = 0; k < 4; k++) o1[k] = src[74 + 4 * s + k];
+    o2[0] = src[66 + s];
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    put_row<F.w[2]>(img2, c, r, o2, keep);
+    // the scale nibbles of the chunk's 8 rows in one word (row r at bits 4 r): byte r / 2 from rows r, r + 1
+    const uint32_t nib = (src[106 + s / 2] >> (4 * (s & 1))) & 0xF;
+    const uint32_t next = (uint32_t)__shfl_down((int)nib, 1);
+    if (!(r & 1)) img3[4 * c + r / 2] = (uint8_t)((nib | (next << 4)) & keep);
+    if (put_d) {
+      od[2 * r] = src[0];
+      od[2 * r + 1] = src[1];
+    }
+  } else if constexpr (TYPE == kIQ4XS) {  // d, scales_h (u16), scales_l[4], qs[128]
+    uint8_t o0[16], o1[1];
+#pragma unroll
+    for (int k = 0; k < 16; k++) o0[k] = src[8 + 16 * s + k];
+    const int sh = src[2] | (src[3] << 8);
+    const int l = ((src[4 + s / 2] >> (4 * (s & 1))) & 0xF) | (((sh >> (2 * s)) & 3) << 4);
+    o1[0] = (uint8_t)(int8_t)(l - 32);
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    if (put_d) {
+      od[2 * r] = src[0];
+      od[2 * r + 1] = src[1];
+    }
+  } else if constexpr (TYPE == kQ2K) {  // scales[16], qs[64], d, dmin
+    // sub-block s = 4 n + j: weights 128 n + 32 j + l = (qs[32 n + l] >> 2 j) & 3. Word h (weights 16 h ..):
+    // byte k holds weights 16 h + k + 4 i at bits 2 i.
+    const int n = s / 4, j = s % 4;
+    const uint8_t* qs = src + 16 + 32 * n;
+    uint8_t o0[8], o1[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint8_t v = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) v |= (uint8_t)(((qs[16 * h + k + 4 * i] >> (2 * j)) & 3) << (2 * i));
+        o0[4 * h + k] = v;
+      }
+    o1[0] = src[8 * n + 2 * j];
+    o1[1] = src[8 * n + 2 * j + 1];
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    if (put_d)
+      for (int k = 0; k < 4; k++) od[4 * r + k] = src[80 + k];
+  } else if constexpr (TYPE == kIQ2XXS) {  // d, per sub-block 4 grid indices + a sign / scale word
+    uint8_t o0[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) o0[k] = src[2 + 8 * s + k];
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    if (put_d) {
+      od[2 * r] = src[0];
+      od[2 * r + 1] = src[1];
+    }
+  } else if constexpr (TYPE == kIQ2XS) {  // d, qs[32] (u16 index + signs), scales[8]
+    uint8_t o0[8], o1[1];
+#pragma unroll
+    for (int k = 0; k < 8; k++) o0[k] = src[2 + 8 * s + k];
+    o1[0] = src[66 + s];
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    if (put_d) {
+      od[2 * r] = src[0];
+      od[2 * r + 1] = src[1];
+    }
+  } else if constexpr (TYPE == kIQ3XXS) {  // d, qs[64], scales_and_signs[32]
+    uint8_t o0[8], o1[4];
+#pragma unroll
+    for (int k = 0; k < 8; k++) o0[k] = src[2 + 8 * s + k];
+#pragma unroll
+    for (int k = 0; k < 4; k++) o1[k] = src[66 + 4 * s + k];
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    if (put_d) {
+      od[2 * r] = src[0];
+      od[2 * r + 1] = src[1];
+    }
+  } else if constexpr (TYPE == kIQ2S) {  // d, qs[32], signs[32], qh[8], scales[8]
+    uint8_t o0[4], o1[4], o2[1], o3[1];
+#pragma unroll
+    for (int k = 0; k < 4; k++) o0[k] = src[2 + 4 * s + k];
+#pragma unroll
+    for (int k = 0; k < 4; k++) o1[k] = src[34 + 4 * s + k];
+    o2[0] = src[66 + s];
+    o3[0] = src[74 + s];
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    put_row<F.w[2]>(img2, c, r, o2, keep);
+    put_row<F.w[3]>(img3, c, r, o3, keep);
+    if (put_d) {
+      od[2 * r] = src[0];
+      od[2 * r + 1] = src[1];
+    }
+  } else if constexpr (TYPE == kIQ1M) {  // qs[32], qh[16], scales[8] (4 x u16, fp16 scale in the top nibbles)
+    uint8_t o0[4], o1[2], o2[1];
+#pragma unroll
+    for (int k = 0; k < 4; k++) o0[k] = src[4 * s + k];
+    o1[0] = src[32 + 2 * s];
+    o1[1] = src[33 + 2 * s];
+    uint16_t s16[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) s16[k] = (uint16_t)(src[48 + 2 * k] | (src[49 + 2 * k] << 8));
+    o2[0] = (uint8_t)((s16[s / 2] >> (6 * (s % 2))) & 63);
+    put_row<F.w[0]>(img0, c, r, o0, keep);
+    put_row<F.w[1]>(img1, c, r, o1, keep);
+    put_row<F.w[2]>(img2, c, r, o2, keep);
+    if (put_d) {
+      const uint16_t dh = (uint16_t)((s16[0] >> 12) | ((s16[1] >> 8) & 0x00F0) | ((s16[2] >> 4) & 0x0F00) | (s16[3] & 0xF000));
+      od[2 * r] = (uint8_t)(dh & 0xFF);
+      od[2 * r + 1] = (uint8_t)(dh >> 8);
+    }
+  }
+  __syncthreads();
+
+  // images -> the fields: wide fields as the group's whole 32 x wf range, narrow ones and the scales for nbg blocks
+  const size_t tb0 = tile * nb + b0;
+  auto out = [&](uint8_t* f, int wf, const uint8_t* img) {
+    if (wf > 16) copy_out(f + (tile * ngroups + g) * 32 * (size_t)wf, img, 32 * wf);
+    else copy_out(f + tb0 * 8 * wf, img, nbg * 8 * wf);
+  };
+  out(f0, F.w[0], img0);
+  if constexpr (F.nf > 1) out(f1, F.w[1], img1);
+  if constexpr (F.nf > 2) out(f2, F.w[2], img2);
+  if constexpr (F.nf > 3) out(f3, F.w[3], img3);
+  copy_out(dd + tb0 * F.dw, imgd, nbg * F.dw);
+}
 // ---------------------------------------------------------------- decode of one chunk
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 // Exact integer product of operands within 24 bits whose product fits 32 bits (v_mul_i32_i24, full rate; a plain
@@ -889,12 +1005,11 @@ extern "C" int q27h_qmat_repack(int type, int N, int K, const void* raw, void* b
   size_t off[5];
   layout(type, N, K, off);
   uint8_t* b = (uint8_t*)buf;
-  const size_t nchunks = (size_t)(N / 8) * (K / 256) * 8;
-  const dim3 grid((unsigned)((nchunks + 255) / 256));
-  const uint8_t* r = (const uint8_t*)raw;
   const int nb = K / 256;
+  const dim3 grid((unsigned)((size_t)(N / 8) * ((nb + kRepackBlocks - 1) / kRepackBlocks)));
+  const uint8_t* r = (const uint8_t*)raw;
 #define Q27H_REPACK(T) hipLaunchKernelGGL(repack_kernel<T>, grid, dim3(256), 0, stream_of(s), r, b + off[0], b + off[1], b + off[2], \
-                                           b + off[3], b + off[4], nb, nchunks)
+                                           b + off[3], b + off[4], nb)
   switch (type) {
     case kQ2K: Q27H_REPACK(kQ2K); break;
     case kQ4K: Q27H_REPACK(kQ4K); break;
