@@ -195,7 +195,8 @@ using namespace q27h;
 
 // Prefill (flip) runs from kChunkMinT tokens on in the chunked form on matrix cores (gdn_chunk.hip), unless the
 // process asked for the sequential, bit-exact kernel. Measured (us, 48 value heads, sequential / chunked): 64 tokens
-// 18.5 / 18.5, 128 tokens 33.9 / 27.7, 512 tokens 125 / 83, 2048 tokens 489 / 294-310.
+// 18.7 / 23.1, 96 tokens 26.4 / 27.0, 128 tokens 33.8 / 30.8, 512 tokens 126 / 77, 2048 tokens 491 / 273, 8192
+// tokens 2008 / 1078.
 constexpr int kChunkMinT = 128;
 static std::atomic<int> g_prefill_exact{0};
 

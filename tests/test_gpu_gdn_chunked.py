@@ -59,7 +59,8 @@ def _f64_recurrence(x, stride, g, beta, planes, in_plane, H, HK, T):
     return o.reshape(-1), S.transpose(0, 2, 1).reshape(-1)
 
 
-@pytest.mark.parametrize("M,in_plane", [(2048, 0), (333, 1), (40, 2), (17, 3), (16, 1), (5, 0), (1, 1)])
+@pytest.mark.parametrize("M,in_plane", [(2048, 0), (333, 1), (64, 0), (63, 3), (40, 2), (32, 1), (17, 3), (16, 1), (5, 0),
+                                        (1, 1)])
 def test_gdn_chunked_vs_sequential_oracle(q27, oracle, dev, M, in_plane):
     H, HK = cd.HV, cd.KH
     say(f"gdn chunked M={M} in_plane={in_plane}")
