@@ -85,6 +85,29 @@ def test_qgemv_small_and_edge_shapes(q27, oracle, dev):
             assert_bits_equal(got, want, f"qgemv edge type {type_} {N}x{K}")
 
 
+def test_qgemv_repack_unaligned_raw(q27, oracle, dev):
+    """The repack reads raw rows at any byte alignment: 4-byte loads when every row start allows them, 2-byte loads
+    (an odd block count of a 2 mod 4 block size, or a raw pointer at 2 mod 4), byte loads for an odd pointer."""
+    import torch
+
+    for type_ in TYPES:
+        for N, K, shift in [(24, 1280, 1), (24, 1280, 2), (16, 2304, 3), (8, 256, 1)]:
+            say(f"qgemv repack unaligned type {type_} {N}x{K} offset {shift}")
+            r = cd.rng(800 + type_ + shift)
+            raw = cd.random_weights(r, type_, N, K, d_range=(-20, 10))
+            xq, xd = cd.q8_activations(oracle, r, 1, K, std=40.0)
+            buf = torch.zeros(raw.size + 16, dtype=torch.uint8, device=dev)
+            draw = buf[shift:shift + raw.size]
+            draw.copy_(torch.from_numpy(raw))
+            assert draw.data_ptr() % 4 == shift % 4
+            m = q27.ops.qmat_upload(draw, type_, N, K)
+            y = torch.full((N,), float("nan"), device=dev)
+            q27.ops.qgemv(m, torch.from_numpy(xq).to(dev), torch.from_numpy(xd).to(dev), y, 1)
+            torch.cuda.synchronize()
+            want = oracle.qgemv(type_, raw, N, K, xq, xd, 1)
+            assert_bits_equal(y.cpu().numpy().reshape(1, N), want, f"repack unaligned {type_} {N}x{K} +{shift}")
+
+
 def test_qgemv_errors(q27, dev):
     import torch
 
