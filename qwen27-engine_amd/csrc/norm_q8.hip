@@ -372,7 +372,9 @@ int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* 
   // 1024-thread form with 5 values per lane, the reference's layout, measured slower: 4.0 against 3.3 us per decode
   // node. A persistent form (a grid of 1-4 workgroups per CU, each walking rows with the next row's loads in flight)
   // measured slower at 2048 rows: 30.0-31.7 against 27.6 us for sum_norm_rows. Fewer resident workgroups per CU
-  // (dynamic LDS of 32, 40 or 54 KB per workgroup) made no difference to the pass; 80 KB made it 8% slower.
+  // (dynamic LDS of 32, 40 or 54 KB per workgroup) made no difference to the pass; 80 KB made it 8% slower. The
+  // in-place x store right after the loads, before the reduction, is worth 140 us per pass against storing x after
+  // it beside the q8_1 output (10.41-10.48 against 10.55-10.61 ms).
   hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
                      xq, xd, xs, wown, wrecv, qb_shift);
   return check_launch(fn);
