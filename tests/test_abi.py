@@ -62,6 +62,14 @@ FAKE = 1 << 20  # an aligned non-null address: the calls below must fail before 
      "bad shape"),
     (lambda o: o.gdn_step(FAKE, FAKE + 8, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 4, 0.088, True, 0), -4,
      "alignment"),
+    (lambda o: o.gdn_step_chunked(FAKE, FAKE, FAKE, 10242, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 2048, 0.088, 0), -1,
+     "bad shape"),
+    (lambda o: o.gdn_step_chunked(FAKE, FAKE, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 65535 * 32 + 1, 0.088, 0), -1,
+     "T too large"),
+    (lambda o: o.gdn_step_chunked(FAKE, FAKE + 8, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 2048, 0.088, 0), -4,
+     "alignment"),
+    (lambda o: o.gdn_step_chunked(FAKE, FAKE, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, None, 48, 16, 2048, 0.088, 0), -4,
+     "null pointer"),
     (lambda o: o.to_q8_wire(FAKE, None, True, FAKE, 4096, 4, 0, 16), -1, "n must be 5120"),
     (lambda o: o.to_q8_wire(FAKE, None, True, FAKE, 5120, 4, 0, 24), -1, "qb must be 16 or 32"),
     (lambda o: o.add_norm_rows_q8(FAKE, FAKE, FAKE, 5120, 4, FAKE, 1e-6, None, FAKE, FAKE, None, 0, 0), -1,
@@ -89,6 +97,7 @@ def test_empty_inputs_are_no_ops(q27):
     q27.ops.get_rows_iq2_s(FAKE, 1640, FAKE, 0, FAKE, 5120, 0)
     q27.ops.attn_prep(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1e-6, 0.6, 24, 4, 16, True, 0)
     q27.ops.gdn_step(FAKE, FAKE, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 0, 0.088, True, 0)
+    q27.ops.gdn_step_chunked(FAKE, FAKE, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 0, 0.088, 0)
 
 
 def test_cpp_dropin_header_compiles(tmp_path):
