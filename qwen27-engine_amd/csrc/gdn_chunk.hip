@@ -140,13 +140,13 @@ __device__ __forceinline__ v4f unit_lower_inverse(const float (*B)[kPP], int r, 
 // 2), then per value head on that key head (their g and beta differ): -A and M by the same waves, the diagonal
 // blocks of Tinv on waves 0 and 2, the lower block on wave 1, P assembled in LDS and written out by all 256 threads.
 // 34 KB of LDS and at most 128 registers per lane let four workgroups share a CU, so the grid of 2048-token layers
-// (16 key heads x 64 chunks) is resident at once: 25.4 us against 31.5 us at three per CU, which took two rounds.
-// The kernel moves 84 MB (k and q rows in, four copies of P out), about 14 us of HBM time.
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) gdn_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                             int stride, const float* __restrict__ g,
-                                                             const float* __restrict__ beta, float* __restrict__ planes,
-                                                             const int* __restrict__ in_plane, float* __restrict__ o,
-                                                             int H, int HK, int T) {
+// (16 key heads x 64 chunks) is resident at once: 25.4 us against 31.5 us at three per CU, where the grid ran as two
+// successive waves of workgroups. The kernel moves 84 MB (k and q rows in, four copies of P out), about 14 us of HBM
+// time.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+gdn_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k, int stride, const float* __restrict__ g,
+                      const float* __restrict__ beta, float* __restrict__ planes, const int* __restrict__ in_plane,
+                      float* __restrict__ o, int H, int HK, int T) {
   // the chunk's k and q rows; once the grams are formed the same LDS holds -A (strictly lower), the diagonal blocks
   // of Tinv and P (34 KB in all: four workgroups per CU)
   __shared__ __align__(16) float smem[2 * kC * kKP];
