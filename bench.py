@@ -918,6 +918,7 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
     ap.add_argument("--repack-only", action="store_true", help="only the qmat_upload repack of each weight type")
+    ap.add_argument("--gdn-only", action="store_true", help="only the delta-rule recurrence legs (for rocprof counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the fused-op path has no multi-GPU form in this build "
@@ -935,6 +936,9 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}")
     if args.repack_only:
         print(json.dumps({"qmat_repack": bench_repack(q27, torch)}), flush=True)
+        return
+    if args.gdn_only:
+        print(json.dumps({"gdn_recurrence": bench_gdn(q27, torch)}), flush=True)
         return
 
     # ---- prefill pass (the step)
