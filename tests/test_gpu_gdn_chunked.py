@@ -77,8 +77,9 @@ def test_gdn_chunked_vs_sequential_oracle(q27, oracle, dev, M, in_plane):
             assert np.array_equal(got_p[p * n:(p + 1) * n].view(np.uint32), planes[p * n:(p + 1) * n].view(np.uint32)), p
 
 
-@pytest.mark.parametrize("M", [333, 40])
+@pytest.mark.parametrize("M", [8192, 333, 40])
 def test_gdn_chunked_vs_float64(q27, dev, M):
+    """M = 8192: 256 chunks, so the state carries the chunked form's rounding through a long sequence."""
     H, HK = cd.HV, cd.KH
     say(f"gdn chunked vs float64 M={M}")
     x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(400 + M), M)
