@@ -562,12 +562,18 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       // all 12 table reads of the row first, then the arithmetic: one LDS wait per row instead of one per lookup
       uint32_t g[8];
       uint2 mm[4];
-      // 9-bit index k = qs byte k | qh bit k << 8, assembled by one byte permute from the qs word and the qh bits
-      // spread to bytes (byte j of hb[h] = bit 4 h + j of qh)
-      const uint32_t hb[2] = {((qh & 0xFu) * 0x204081u) & 0x01010101u, ((qh >> 4) * 0x204081u) & 0x01010101u};
+      if constexpr (NC < 4) {
+        // 9-bit index k = qs byte k | qh bit k << 8, assembled by one byte permute from the qs word and the qh bits
+        // spread to bytes (byte j of hb[h] = bit 4 h + j of qh). With four columns the two extra live words per row
+        // raise the kernel's spill from 12 to 28 bytes per lane, so that form keeps the shifts.
+        const uint32_t hb[2] = {((qh & 0xFu) * 0x204081u) & 0x01010101u, ((qh >> 4) * 0x204081u) & 0x01010101u};
 #pragma unroll
-      for (int k = 0; k < 8; k++)
-        g[k] = lut[__builtin_amdgcn_perm(hb[k / 4], w[2 * r + k / 4], 0x0C0C0000u | ((4u + (k & 3)) << 8) | (k & 3))];
+        for (int k = 0; k < 8; k++)
+          g[k] = lut[__builtin_amdgcn_perm(hb[k / 4], w[2 * r + k / 4], 0x0C0C0000u | ((4u + (k & 3)) << 8) | (k & 3))];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; k++) g[k] = lut[((w[2 * r + k / 4] >> (8 * (k & 3))) & 0xFF) | ((qh << (8 - k)) & 0x100)];
+      }
 #pragma unroll
       for (int p = 0; p < 4; p++) mm[p] = smask[(sg >> (8 * p)) & 0xFF];
       int sumi[NC];
