@@ -487,6 +487,9 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
                                           float (&acc)[8 * NC]) {
   const uint32_t* w = ch.w;
   if constexpr (TYPE == kQ4K) {
+    // (the min term's (float)(s8 * m) equals (float)s8 * (float)m exactly, |s8 * m| < 2^24; that form, one multiply
+    // instead of a 24-bit multiply and a conversion per row and column, measured slower: 5120 x 17408 T = 4 20.3
+    // against 18.8 us)
     int s8[NC];  // sums of the activations: the min term (dmin * m) multiplies them
 #pragma unroll
     for (int c = 0; c < NC; c++) {
