@@ -631,6 +631,8 @@ def bench_gdn(q27, torch, M=2048):
                                          "GBps": round(b / us_seq / 1e3, 1)}
             # multiply-adds of the three state products (K S, Q S, K^T Delta) per token and head, fp32 matrix cores
             out[name]["state_products_TFLOPs"] = round(3 * 2 * D * D * T * H / (us * 1e-6) / 1e12, 2)
+            # the same as a share of the dense fp32 matrix-core peak (157.3 TFLOP/s)
+            out[name]["state_products_frac_fp32_mfma_peak"] = round(out[name]["state_products_TFLOPs"] / 157.3, 4)
             log(f"  gdn_step {name + '_sequential':9s} T={T:5d} {us_seq:8.2f} us ({us_seq / T:.3f} us/token)")
     return out
 
