@@ -9,14 +9,22 @@
  *   q27o_expf, q27o_logf, q27o_sincos  ulp distance to glibc expf/logf and to sin/cos in long double
  *   q27o_f2h / q27o_h2f / q27o_f2bf   exhaustive round trip over all 65536 codes + RNE ties vs numpy
  *   q8_1 (quantize_q8_1, q8_store)    closed-form blocks (zero, one-hot, ties), |q| <= 127, xd = fp16(d)
- *                                     vs numpy float16, xs vs an independent butterfly transcription
+ *                                     vs numpy float16, roundf(y / d) vs numpy's quotient on near-tie blocks;
+ *                                     xs by blocks whose xor 8-4-2-1 sums are derived by hand
+ *                                     (tests/treepins.py, test_oracle_trees.py)
  *   rmsnorm / rmsnorm_q8 / sum_norm*  constant-row closed form, mean(h^2) = m/(m+eps) invariant, fused ==
- *                                     unfused chain (tools/test_fused.cu:55-74), reduction tree vs brute force
+ *                                     unfused chain (tools/test_fused.cu:55-74); the reduction tree (strided
+ *                                     per-thread partials, warp and cross-warp butterflies) by rows whose sums of
+ *                                     squares are derived by hand for that tree and differ for a sequential sum,
+ *                                     a contiguous layout or a reversed per-thread order; (scale * v) * w by
+ *                                     integer rows (test_oracle_trees.py)
  *   swiglu(_q8)                       silu(0) = 0, asymptotes, fused == swiglu + quantize_q8_1
- *   gated_rmsnorm(_q8)                w = 1 / large z reduces to RMSNorm, fused == unfused + quantize
- *   l2norm_heads, gdn_conv*, gates    sum y^2 = S/(S+eps) per head, fused == unfused
+ *   gated_rmsnorm(_q8)                w = 1 / large z reduces to RMSNorm, fused == unfused + quantize; the
+ *                                     4-warp tree and the product order as for the rows
+ *   l2norm_heads, gdn_conv*, gates    sum y^2 = S/(S+eps) per head, fused == unfused, the strided-lane tree
  *                                     (tools/test_fused.cu:76-102), decode == prefill conv on the same rows
- *   attn_prep                         pair norms preserved by RoPE, p = 0 identity, rope3 with t=h=w == plain
+ *   attn_prep                         8-warp head-norm tree and (scale * v) * w as for the rows; pair norms
+ *                                     preserved by RoPE, p = 0 identity, rope3 with t=h=w == plain
  *                                     positions, q8_0/f16 cache special cases, numpy float64 rotation bound
  *   get_rows_*                        hand-built one-hot blocks decoded by brute force, Q8_0 closed form
  */
