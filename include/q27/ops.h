@@ -64,7 +64,9 @@ inline void gdn_conv(const float* x, const float* w, float* planes, const int* i
                      bool snapshots, hipStream_t s) {
   q27h_check(q27h_gdn_conv(x, w, planes, in_plane, y, C, T, snapshots ? 1 : 0, s));
 }
-// src/ops.h:40-45
+// src/ops.h:40-45. With flip and T >= 128 this runs the chunked form on matrix cores (unless gdn_prefill_exact(true)
+// or o overlaps an input): o and the final state then agree with the sequential kernel within float32 rounding
+// (relative 1e-5 per 128-value vector), not bit for bit, and T may be at most 65535 * 32.
 inline void gdn_step(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
                      float* planes, const int* in_plane, float* o, int H, int HK, int T, float scale, bool snapshots,
                      hipStream_t s, bool flip = false) {
@@ -72,7 +74,8 @@ inline void gdn_step(const float* q, const float* k, const float* v, int stride,
                            flip ? 1 : 0));
 }
 // No counterpart in the reference: gdn_step's prefill sequential and bit-exact (true) or chunked on matrix cores
-// from 128 tokens on (false, the default), process-wide; returns the previous setting.
+// from 128 tokens on (false, the default), process-wide; returns the previous setting. Read when a gdn_step call
+// enqueues its launch, not at graph replay; threads that change it race with other threads' calls.
 inline bool gdn_prefill_exact(bool on) { return q27h_gdn_prefill_exact(on ? 1 : 0) != 0; }
 // src/ops.h:36
 inline void l2norm_heads(float* x, int n, int heads, int T, int stride, float eps, hipStream_t s) {

@@ -99,7 +99,11 @@ int q27h_gdn_conv(const float* x, const float* w, float* planes, const int* in_p
  * of 128 x 128 f32 state (value head h uses key head h % HK); q / k / v rows of `stride` floats (q, k at
  * kh * 128, v at h * 128), g / beta [T][H], o [T][H][128] = (S^T q) * scale. planes [4][H][128 col][128 i].
  * flip = 0 (decode, T <= 4): read plane *in_plane, write plane t after token t when snapshots, else plane T - 1.
- * flip = 1 (prefill, any T): the final state goes to plane (*in_plane == 0 ? 1 : 0); no snapshots.
+ * flip = 1 (prefill, any T): the final state goes to plane (*in_plane == 0 ? 1 : 0); no snapshots. From T >= 128 on
+ * this runs q27h_gdn_step_chunked (below) unless q27h_gdn_prefill_exact(1) was called or o overlaps an input: o and the
+ * final state then agree with the sequential kernel within float32 rounding (relative 1e-5 per 128-value vector), not
+ * bit for bit, and T is limited to 65535 * 32. Below 128 tokens, in exact mode or with an overlapping o, the
+ * sequential kernel runs and its results are bit-exact against the CPU checker.
  * q, k and planes 16-byte aligned, stride % 4 == 0. */
 int q27h_gdn_step(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
                   float* planes, const int* in_plane, float* o, int H, int HK, int T, float scale, int snapshots,
@@ -107,15 +111,19 @@ int q27h_gdn_step(const float* q, const float* k, const float* v, int stride, co
 /* gdn_step's prefill (flip) mode in the chunked form on matrix cores: no counterpart in the reference, whose
  * prefill kernel runs token by token (src/ops.cu:449-572). Same arguments, outputs and plane semantics as
  * q27h_gdn_step with flip = 1 and snapshots = 0; the additions happen in another order, so o and the final state
- * agree with the sequential form to float32 rounding (relative 1e-5 of the largest value), not bit for bit.
- * q27h_gdn_step with flip = 1 takes this path for T >= 128 unless q27h_gdn_prefill_exact(1) was called. o must not
- * overlap the inputs (the chunks' matrices are staged in o before the outputs overwrite them). */
+ * agree with the sequential form to float32 rounding (relative 1e-5 per 128-value vector: a (token, head) row of o,
+ * a state column), not bit for bit. q27h_gdn_step with flip = 1 takes this path for T >= 128 unless
+ * q27h_gdn_prefill_exact(1) was called. o may share no byte with the q / k / v rows, g, beta or the planes (the
+ * chunks' matrices are staged in o before the outputs overwrite them): Q27H_ERR_ARG otherwise. T <= 65535 * 32. */
 int q27h_gdn_step_chunked(const float* q, const float* k, const float* v, int stride, const float* g,
                           const float* beta, float* planes, const int* in_plane, float* o, int H, int HK, int T,
                           float scale, q27h_stream_t s);
 /* Process-wide choice for gdn_step's prefill (flip) mode: 1 = always the sequential kernel (bit-exact against the
  * CPU checker), 0 (the default) = the chunked form from 128 tokens on. Returns the previous setting. No counterpart
- * in the reference (its prefill is sequential); for callers that need the sequential bits. */
+ * in the reference (its prefill is sequential); for callers that need the sequential bits. The setting is read when
+ * q27h_gdn_step enqueues its launch: a graph captured under one setting keeps that path at every replay, and a thread
+ * that changes it races with other threads' calls (a caller that needs a fixed path can call
+ * q27h_gdn_step_chunked directly, or set exact mode once at start-up). */
 int q27h_gdn_prefill_exact(int on);
 /* gdn_conv_l2 (src/ops.h:112-114, src/ops.cu:731-737): gdn_conv + l2norm_heads of the first n_norm_heads heads
  * + gdn_gates in one launch. C % 128 == 0 and C / 128 - n_norm_heads == H. pf/pf_bytes ignored. */

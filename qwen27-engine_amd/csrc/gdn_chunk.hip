@@ -460,6 +460,18 @@ __global__ void __launch_bounds__(512) gdn_chunk_kernel(const float* __restrict_
 
 using namespace q27h;
 
+// The chunked form parks each chunk's matrices in o's rows before the outputs overwrite them, so o may share no
+// byte with what the launches read: the q / k / v rows, g, beta and the four state planes.
+bool q27h::gdn_chunk_o_overlaps(const float* q, const float* k, const float* v, int stride, const float* g,
+                                const float* beta, const float* planes, const float* o, int H, int HK, int T) {
+  const size_t fb = sizeof(float);
+  const size_t rows = (size_t)(T - 1) * stride;
+  const size_t ob = (size_t)T * H * 128 * fb;
+  return overlaps(o, ob, q, (rows + (size_t)HK * 128) * fb) || overlaps(o, ob, k, (rows + (size_t)HK * 128) * fb) ||
+         overlaps(o, ob, v, (rows + (size_t)H * 128) * fb) || overlaps(o, ob, g, (size_t)T * H * fb) ||
+         overlaps(o, ob, beta, (size_t)T * H * fb) || overlaps(o, ob, planes, (size_t)4 * H * 128 * 128 * fb);
+}
+
 extern "C" int q27h_gdn_step_chunked(const float* q, const float* k, const float* v, int stride, const float* g,
                                      const float* beta, float* planes, const int* in_plane, float* o, int H, int HK,
                                      int T, float scale, q27h_stream_t s) {
@@ -469,6 +481,8 @@ extern "C" int q27h_gdn_step_chunked(const float* q, const float* k, const float
   if (!aligned16(q) || !aligned16(k) || !aligned16(planes))
     return fail(Q27H_ERR_ARG, "gdn_step_chunked: q, k and planes need 16-byte alignment");
   if (T > 65535 * kC) return fail(Q27H_ERR_SHAPE, "gdn_step_chunked: T too large");
+  if (gdn_chunk_o_overlaps(q, k, v, stride, g, beta, planes, o, H, HK, T))
+    return fail(Q27H_ERR_ARG, "gdn_step_chunked: o overlaps q / k / v rows, g, beta or the state planes");
   const hipStream_t st = stream_of(s);
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(min(H, HK), (T + kC - 1) / kC), dim3(256), 0, st, q, k, stride, g, beta,
                      planes, in_plane, o, H, HK, T);

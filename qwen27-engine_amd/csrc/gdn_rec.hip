@@ -211,7 +211,9 @@ extern "C" int q27h_gdn_step(const float* q, const float* k, const float* v, int
   if (!q || !k || !v || !g || !beta || !planes || !in_plane || !o) return fail(Q27H_ERR_ARG, "gdn_step: null pointer");
   if (!aligned16(q) || !aligned16(k) || !aligned16(planes))
     return fail(Q27H_ERR_ARG, "gdn_step: q, k and planes need 16-byte alignment");
-  if (flip && T >= kChunkMinT && !g_prefill_exact.load(std::memory_order_relaxed))
+  // the switch is read here, when the launch is enqueued: a graph captured under one setting keeps its path
+  if (flip && T >= kChunkMinT && !g_prefill_exact.load(std::memory_order_relaxed) &&
+      !gdn_chunk_o_overlaps(q, k, v, stride, g, beta, planes, o, H, HK, T))
     return q27h_gdn_step_chunked(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, s);
   if (!flip && snapshots && T > 1)
     hipLaunchKernelGGL((gdn_rec_kernel<kParts, true>), dim3(H, 128 / kCols), dim3(kCols * kParts), 0, stream_of(s), q, k,

@@ -16,5 +16,14 @@ int check_launch(const char* what);
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 inline hipStream_t stream_of(q27h_stream_t s) { return (hipStream_t)s; }
+// True when the byte ranges [a, a + na) and [b, b + nb) share a byte.
+inline bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return na && nb && x < y + nb && y < x + na;
+}
+
+// gdn_chunk.hip: whether o shares memory with an input of the chunked delta-rule prefill (which it may not).
+bool gdn_chunk_o_overlaps(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
+                          const float* planes, const float* o, int H, int HK, int T);
 
 }  // namespace q27h

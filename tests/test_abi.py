@@ -70,6 +70,11 @@ FAKE = 1 << 20  # an aligned non-null address: the calls below must fail before 
      "alignment"),
     (lambda o: o.gdn_step_chunked(FAKE, FAKE, FAKE, 10240, FAKE, FAKE, FAKE, FAKE, None, 48, 16, 2048, 0.088, 0), -4,
      "null pointer"),
+    # o may not share memory with the rows, gates or planes it is staged beside (here o lies inside the q rows)
+    (lambda o: o.gdn_step_chunked(FAKE, FAKE + 4096, FAKE + 8192, 10240, 1 << 30, (1 << 30) + (1 << 24), 1 << 31,
+                                  FAKE, FAKE + 65536, 48, 16, 2048, 0.088, 0), -4, "overlaps"),
+    (lambda o: o.gdn_step_chunked(FAKE, FAKE + 4096, FAKE + 8192, 10240, 1 << 30, (1 << 30) + (1 << 24), 1 << 31,
+                                  FAKE, (1 << 31) + (1 << 20), 48, 16, 2048, 0.088, 0), -4, "overlaps"),
     (lambda o: o.to_q8_wire(FAKE, None, True, FAKE, 4096, 4, 0, 16), -1, "n must be 5120"),
     (lambda o: o.to_q8_wire(FAKE, None, True, FAKE, 5120, 4, 0, 24), -1, "qb must be 16 or 32"),
     (lambda o: o.add_norm_rows_q8(FAKE, FAKE, FAKE, 5120, 4, FAKE, 1e-6, None, FAKE, FAKE, None, 0, 0), -1,

@@ -1,7 +1,15 @@
 """GPU checks of the chunked prefill form of the delta rule (q27h_gdn_step_chunked through the C ABI): o and the
 final state against the sequential CPU oracle (itself pinned bit for bit against the sequential GPU kernel and by a
-float64 recurrence) within float32 rounding, relative 1e-5 of the largest value (the north_star's fp32 tolerance),
-and against a float64 recurrence; plane semantics bit for bit (only the other of planes 0 / 1 is written)."""
+float64 recurrence) and against a float64 recurrence; plane semantics bit for bit (only the other of planes 0 / 1 is
+written).
+
+Tolerance, per 128-value vector (one (token, head) row of o, one state column of a head), so that a wrong block fails
+on its own whatever the other heads hold: |got - want| <= RTOL * A for every value, A the vector's largest magnitude.
+RTOL is 1e-5 (the north_star's fp32 bar) against a float64 recurrence, and 2e-5 against the sequential float32 oracle
+(both float32 forms are within 1e-5 of the exact values). Relative 1e-5 per value is not a bar that float32 can meet
+here: o's small values are differences of larger terms, and the sequential float32 order of the reference itself is
+off the float64 result by up to 6.6e-5 relative on values above 1/64 of their vector's maximum (M = 2048). The
+per-value figures of both forms are printed beside each check."""
 import sys
 
 import numpy as np
@@ -12,7 +20,9 @@ import cfgdata as cd
 pytestmark = pytest.mark.gpu
 
 SCALE = np.float32(1.0 / np.sqrt(128.0))
-RTOL = 1e-5  # of the largest |value| of the compared array
+RTOL_F64 = 1e-5   # against the float64 recurrence
+RTOL_SEQ = 2e-5   # against the sequential float32 oracle
+FLOOR = 2.0 ** -6  # values reported per value: those above FLOOR of their vector's maximum
 
 
 def say(msg):
@@ -33,13 +43,23 @@ def _run(q27, dev, x, stride, g, beta, planes, in_plane, H, HK, T):
     return o.cpu().numpy()[: T * H * 128], dp.cpu().numpy()
 
 
-def _close(got, want, what):
+def _close(got, want, what, rtol=RTOL_SEQ):
+    """Per 128-value vector: |got - want| <= rtol * (the vector's largest |want|). Returns the largest error relative
+    to its vector's maximum; prints it with the largest per-value relative error of values above FLOOR of it."""
     assert np.all(np.isfinite(got)), f"{what}: non-finite values"
-    err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
-    ref = np.abs(want.astype(np.float64)).max()
-    assert err <= RTOL * ref, f"{what}: max error {err:.3e} > {RTOL} x {ref:.3e}"
-    return err / ref
-
+    g = got.astype(np.float64).reshape(-1, 128)
+    w = want.astype(np.float64).reshape(-1, 128)
+    err = np.abs(g - w)
+    vmax = np.abs(w).max(1, keepdims=True)
+    bad = np.argwhere(err > rtol * vmax)
+    rel_blk = (err / np.where(vmax > 0, vmax, 1)).max()
+    big = np.abs(w) >= FLOOR * vmax
+    rel_el = (err[big] / np.abs(w[big])).max() if big.any() else 0.0
+    say(f"{what}: max error / vector max {rel_blk:.2e} (bound {rtol:g}); max relative error of values >= "
+        f"{FLOOR} x max {rel_el:.2e}")
+    assert bad.size == 0, (f"{what}: {len(bad)} values outside the bound; first vector {bad[0][0]} index {bad[0][1]}: "
+                           f"{g[tuple(bad[0])]!r} vs {w[tuple(bad[0])]!r} (vector max {vmax[bad[0][0], 0]:.3e})")
+    return rel_blk
 
 def _f64_recurrence(x, stride, g, beta, planes, in_plane, H, HK, T):
     """The delta rule in float64 (delta = (v - e^g S^T k) beta, S <- e^g S + k delta^T, o = scale S^T q)."""
@@ -86,8 +106,8 @@ def test_gdn_chunked_vs_float64(q27, dev, M):
     got_o, got_p = _run(q27, dev, x, stride, g, beta, planes, 0, H, HK, M)
     want_o, want_s = _f64_recurrence(x, stride, g, beta, planes, 0, H, HK, M)
     n = H * 128 * 128
-    _close(got_o, want_o, f"o vs float64 M={M}")
-    _close(got_p[n:2 * n], want_s, f"state vs float64 M={M}")
+    _close(got_o, want_o, f"o vs float64 M={M}", RTOL_F64)
+    _close(got_p[n:2 * n], want_s, f"state vs float64 M={M}", RTOL_F64)
 
 
 def test_gdn_chunked_edge_values(q27, oracle, dev):
@@ -105,6 +125,9 @@ def test_gdn_chunked_edge_values(q27, oracle, dev):
     n = H * 128 * 128
     _close(got_o, want_o, "edge o")
     _close(got_p[n:2 * n], want_p[n:2 * n], "edge state")
+    f_o, f_s = _f64_recurrence(x, stride, g, beta, planes, 0, H, HK, M)
+    _close(got_o, f_o, "edge o vs float64", RTOL_F64)
+    _close(got_p[n:2 * n], f_s, "edge state vs float64", RTOL_F64)
 
 
 def _run_step(q27, dev, x, stride, g, beta, planes, in_plane, H, HK, T):
@@ -177,3 +200,37 @@ def test_gdn_chunked_replays_in_hip_graph(q27, dev):
         torch.cuda.synchronize()
         assert np.array_equal(o.cpu().numpy().view(np.uint32), want_o.view(np.uint32)), "graph replay o"
         assert np.array_equal(dp.cpu().numpy().view(np.uint32), want_p.view(np.uint32)), "graph replay planes"
+
+
+def test_gdn_chunked_downstream_int8(q27, oracle, dev):
+    """How many int8 values of the next op (gated_rmsnorm_q8 of o, src/model.cu's order) differ between the chunked
+    and the sequential prefill at M = 2048: a value differs only where o's rounding moves y / d across a half-integer,
+    so a small share is expected; the count is reported and bounded, the scales of the blocks checked."""
+    import torch
+
+    H, HK, M = cd.HV, cd.KH, 2048
+    say(f"gdn chunked vs sequential, downstream gated_rmsnorm_q8 int8 M={M}")
+    x, stride, g, beta, planes = cd.gdn_inputs(cd.rng(800), M)
+    ch_o, _ = _run(q27, dev, x, stride, g, beta, planes, 0, H, HK, M)
+    prev = q27.ops.gdn_prefill_exact(True)
+    try:
+        sq_o, _ = _run_step(q27, dev, x, stride, g, beta, planes, 0, H, HK, M)
+    finally:
+        q27.ops.gdn_prefill_exact(prev)
+    r = cd.rng(801)
+    w = torch.from_numpy((1 + 0.1 * r.standard_normal(128)).astype(np.float32)).to(dev)
+    z = torch.from_numpy(r.standard_normal(M * H * 128).astype(np.float32)).to(dev)
+    out = []
+    for o in (ch_o, sq_o):
+        xq = torch.zeros(M * H * 128, dtype=torch.int8, device=dev)
+        xd = torch.zeros(M * H * 4, device=dev)
+        q27.ops.gated_rmsnorm_q8(torch.from_numpy(o).to(dev), w, z, xq, xd, M * H, cd.EPS)
+        torch.cuda.synchronize()
+        out.append((xq.cpu().numpy().astype(np.int32), xd.cpu().numpy()))
+    dq = np.abs(out[0][0] - out[1][0])
+    frac = np.count_nonzero(dq) / dq.size
+    dscale = np.count_nonzero(out[0][1] != out[1][1]) / out[0][1].size
+    say(f"int8 values differing: {np.count_nonzero(dq)} of {dq.size} ({frac:.2e}), max |diff| {dq.max()}; "
+        f"fp16 block scales differing: {dscale:.2e}")
+    assert dq.max() <= 1
+    assert frac < 1e-3
