@@ -798,70 +798,6 @@ def bench_isolated(q27, torch, P, reps=3):
     return out
 
 
-def bench_stream_ceilings(torch, P, isolated, reps=3):
-    """The same bytes as each prefill op moved by a streaming kernel without arithmetic (lib/libq27probe.so, built
-    beside the library for measurement only): the op's reads as 16-byte nontemporal loads, its f32 writes as 16-byte
-    stores, its q8_1 output (int8 per value, f32 per 32 and per 16 values) at the fused ops' granularity, over the
-    same cycled buffers as the isolated leg. `of_stream` = stream time / op time: how close the op comes to what
-    HBM delivers for its mix of reads and writes on this box. The conv, attn_prep and gather rows approximate their
-    access shapes (column tiles and window rows, strided heads, id-dependent rows) by flat streams of equal bytes."""
-    import ctypes as ct
-
-    lib = ct.CDLL(os.path.join(PKG_DIR, "lib", "libq27probe.so"))
-    lib.q27p_flat.argtypes = [ct.c_void_p] * 7 + [ct.c_size_t, ct.c_int, ct.c_int, ct.c_void_p]
-    ptr = lambda t: None if t is None else ct.c_void_p(t.data_ptr())  # noqa: E731
-    M = P.M
-    cyc = lambda seq, i: seq[i % len(seq)]  # noqa: E731
-    nrow, nff, nq, ng = M * E, M * FF, M * NQH * 256, M * HV * D
-    # op: (n, nin, nout, q8 with xs, inputs of launch i, outputs of launch i); rmw ops write their first input
-    shapes = {
-        "sum_norm_rows": (nrow, 2, 1, True, lambda i: (cyc(P.xs_ring, i), cyc(P.m_outs, 8 * i + 1)),
-                          lambda i: (cyc(P.xs_ring, i), None)),
-        "rmsnorm_q8": (nrow, 1, 1, True, lambda i: (cyc(P.xs_ring, i), None), lambda i: (P.h, None)),
-        "swiglu_q8": (nff, 2, 0, True, lambda i: cyc(P.fgus, i), lambda i: (None, None)),
-        "quantize_q8_1": (nq, 1, 0, True, lambda i: (cyc(P.attn_os, i), None), lambda i: (None, None)),
-        "gated_rmsnorm_q8": (ng, 2, 0, True, lambda i: cyc(P.ozs, i), lambda i: (None, None)),
-        "gdn_conv_prefill": (M * C, 1, 1, False, lambda i: (cyc(P.qkvs, i), None), lambda i: (P.conv, None)),
-        "attn_prep": (nq + 2 * M * NKVH * 256, 1, 1, False, lambda i: (cyc(P.qkvas, i)[0], None), lambda i: (P.qn, None)),
-        "get_rows_iq2_s": (nrow, 0, 1, False, lambda i: (None, None), lambda i: (cyc(P.xs_ring, i), None)),
-    }
-    out = {}
-    for name, (n, nin, nout, q8, ins, outs) in shapes.items():
-        if name not in isolated:
-            continue
-        n = n // 1024 * 1024
-        nl = 16
-
-        def launch(i):
-            a, b = ins(i)
-            o0, o1 = outs(i)
-            rc = lib.q27p_flat(ptr(a), ptr(b), ptr(o0), ptr(o1), ptr(P.xq) if q8 else None, ptr(P.xd) if q8 else None,
-                               ptr(P.xs) if q8 else None, n, nin, nout, ct.c_void_p(torch.cuda.current_stream().cuda_stream))
-            if rc:
-                raise RuntimeError(f"stream probe {name}: status {rc}")
-        for i in range(3):
-            launch(i)
-        best = 1e30
-        for _ in range(reps):
-            ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            ea.record()
-            for i in range(nl):
-                launch(i)
-            eb.record()
-            torch.cuda.synchronize()
-            best = min(best, ea.elapsed_time(eb) * 1e3 / nl)
-        nb = n * (4 * nin + 4 * nout + ((1 + 1 / 8 + 1 / 4) if q8 else 0))
-        op = isolated[name]
-        # scale the stream's time to the op's algorithmic bytes before comparing
-        us_eq = best * op["bytes_per_launch"] / nb
-        out[name] = {"stream_us": round(best, 2), "stream_GBps": round(nb / best / 1e3, 1),
-                     "stream_hbm_frac": round(nb / best / 1e3 / HBM_PEAK_GBS, 3),
-                     "op_of_stream": round(us_eq / op["us"], 3)}
-        log(f"  stream {name:18s} {best:8.2f} us  {nb / best / 1e3:8.1f} GB/s; op at {us_eq / op['us']:.1%} of it")
-    P.reset()
-    return out
-
-
 def bench_cfg1(q27, torch):
     """RMSNorm -> q8_1 of one 5120 row (0.1% outliers x50) on the CPU oracle and on the GPU, with the
     bit-exact comparison of xq / xd / xs."""
@@ -1000,7 +936,6 @@ def main():
             f"net {net:7.2f} us ({gbs_net / HBM_PEAK_GBS:.1%})")
     # ---- each op alone (MALL-proof), and the pass with one set of buffers reused by every layer (warm)
     isolated = bench_isolated(q27, torch, P)
-    ceilings = bench_stream_ceilings(torch, P, isolated)
     Pw = Pass(q27, torch, 2048, decode=False, cold=False)
     for _ in range(2):
         Pw.run()
@@ -1131,7 +1066,6 @@ def main():
         "us_per_2048_batch_warm": round(warm_us, 1),
         "per_op": per_op,
         "per_op_isolated": isolated,
-        "stream_ceilings": ceilings,
         "per_op_event_overhead_us": round(ev_overhead_us, 2),
         "decode_per_op": decode_ops,
         "cfg1_rmsnorm_q8_row": cfg1,
