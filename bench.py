@@ -759,6 +759,39 @@ def bench_wire(q27, torch, M=2048):
     return out
 
 
+def bench_decode_graph(q27, torch, replays):
+    """The decode verify pass (T = 4): its launches recorded in one HIP graph, median replay time over `replays`
+    replays, then the per-op node costs."""
+    Dp = Pass(q27, torch, 4, decode=True)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        Dp.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            Dp.run()
+    torch.cuda.synchronize()
+    for _ in range(5):
+        graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) * 1e3)
+    times.sort()
+    decode_us = times[len(times) // 2]
+    log(f"decode verify pass: {len(Dp.launches)} launches in one graph, median {decode_us:.1f} us")
+    del graph
+    decode_ops = bench_decode_ops(q27, torch, Dp)
+    del Dp
+    torch.cuda.empty_cache()
+    return decode_us, decode_ops
+
+
 def bench_isolated(q27, torch, P, reps=3):
     """Every prefill op alone: all of its launches of the cold pass back to back between two HIP events (distinct
     inputs per launch, so the MALL does not serve them: 48-128 launches of 42-285 MB each), best of `reps` rounds.
@@ -856,6 +889,9 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
     ap.add_argument("--repack-only", action="store_true", help="only the qmat_upload repack of each weight type")
+    ap.add_argument("--decode-only", action="store_true", help="only the decode verify pass (T = 4) graph")
+    ap.add_argument("--isolated-only", action="store_true",
+                    help="only the per-op isolated legs of the prefill pass (each op's launches back to back)")
     ap.add_argument("--gdn-only", action="store_true", help="only the delta-rule recurrence legs (for rocprof counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -875,12 +911,22 @@ def main():
     if args.repack_only:
         print(json.dumps({"qmat_repack": bench_repack(q27, torch)}), flush=True)
         return
+    if args.decode_only:
+        decode_us, decode_ops = bench_decode_graph(q27, torch, args.graph_replays)
+        print(json.dumps({"decode_us_per_step": round(decode_us, 1), "decode_per_op": decode_ops}), flush=True)
+        return
     if args.gdn_only:
         print(json.dumps({"gdn_recurrence": bench_gdn(q27, torch)}), flush=True)
         return
 
     # ---- prefill pass (the step)
     P = Pass(q27, torch, 2048, decode=False, cold=args.buffers == "cold")
+    if args.isolated_only:
+        for _ in range(args.warmup):
+            P.run()
+        torch.cuda.synchronize()
+        print(json.dumps({"per_op_isolated": bench_isolated(q27, torch, P)}), flush=True)
+        return
     step_bytes = P.bytes_per_step()
     log(f"prefill pass: {len(P.launches)} launches, {step_bytes / 1e9:.3f} GB algorithmic per step")
     for _ in range(args.warmup):
@@ -981,33 +1027,7 @@ def main():
     torch.cuda.empty_cache()
 
     # ---- decode verify pass (T = 4) in one HIP graph
-    Dp = Pass(q27, torch, 4, decode=True)
-    s = torch.cuda.Stream()
-    with torch.cuda.stream(s):
-        Dp.run()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=s):
-            Dp.run()
-    torch.cuda.synchronize()
-    for _ in range(5):
-        graph.replay()
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(args.graph_replays):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        graph.replay()
-        b.record()
-        b.synchronize()
-        times.append(a.elapsed_time(b) * 1e3)
-    times.sort()
-    decode_us = times[len(times) // 2]
-    log(f"decode verify pass: {len(Dp.launches)} launches in one graph, median {decode_us:.1f} us")
-    del graph
-    decode_ops = bench_decode_ops(q27, torch, Dp)
-    del Dp
-    torch.cuda.empty_cache()
+    decode_us, decode_ops = bench_decode_graph(q27, torch, args.graph_replays)
 
     # ---- configs[0], configs[3] (gathers) and configs[4] (multimodal + GDN)
     cfg1 = bench_cfg1(q27, torch)

@@ -73,8 +73,10 @@ inline void gdn_step(const float* q, const float* k, const float* v, int stride,
   q27h_check(q27h_gdn_step(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, snapshots ? 1 : 0, s,
                            flip ? 1 : 0));
 }
-// No counterpart in the reference: gdn_step's prefill sequential and bit-exact (true) or chunked on matrix cores
-// from 128 tokens on (false, the default), process-wide; returns the previous setting. Read when a gdn_step call
+// No counterpart in the reference: the GDN prefill path bit-exact against the checker (true: gdn_step's prefill
+// sequential, gdn_conv_prefill's SiLU correctly rounded) or the faster forms within float32 rounding (false, the
+// default: the chunked recurrence on matrix cores from 128 tokens on, the hardware-exp SiLU), process-wide; returns
+// the previous setting. Read when a gdn_step call
 // enqueues its launch, not at graph replay; threads that change it race with other threads' calls.
 inline bool gdn_prefill_exact(bool on) { return q27h_gdn_prefill_exact(on ? 1 : 0) != 0; }
 // src/ops.h:36

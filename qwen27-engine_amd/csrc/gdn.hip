@@ -70,7 +70,11 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
 // slower: 41-54 against 37.4 us at M = 2048. Spans of 4 tokens (64 VGPRs, 8 waves per SIMD) measured 37.2 us against
 // 39.2 / 37.3 / 37.9 us for spans of 3 / 5 / 8 and 10.43-10.46 against 10.47-10.54 ms per prefill pass for 8; the
 // token loop without a branch per token (the out-of-range silu redone after the stores) measured the same (37.1 us).
-template <int SPAN>
+// FAST: the SiLU in silu_tol (hardware exp2 and reciprocal, a Newton step; within a few float32 ulps instead of the
+// checker's bits): 35.6-36.0 against 37.3-37.4 us at M = 2048, and 40-50 us less per prefill pass; the same kernel
+// with no SiLU at all ran 34.7-35.0 us, so what remains above a copy of its access shape is the conv, the L2 norm
+// and the stream itself.
+template <int SPAN, bool FAST>
 __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __restrict__ x, const float* __restrict__ cw,
                                                                float* __restrict__ planes, const int* __restrict__ in_plane,
                                                                float* __restrict__ y, int C, int T, int n_norm_heads,
@@ -141,7 +145,8 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
       cv[k] = conv4(s0[k], s1[k], s2[k], xr[i][k], w[k]);
       s0[k] = s1[k]; s1[k] = s2[k]; s2[k] = xr[i][k];
     }
-    q27_silu_n(cv, cur);
+    if constexpr (FAST) q27_silu_tol_n(cv, cur);
+    else q27_silu_n(cv, cur);
     if (norm) l2_head_lanes(cur, eps);
     float* yr = y + (size_t)t * C + cb;
 #pragma unroll
@@ -338,8 +343,16 @@ extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* plan
   const int gate_blocks = (int)(((long)M * H + 255) / 256);
   const int nspans = (M + span - 1) / span;
   const long tiles = ((long)((C / 128 + 7) / 8) * nspans + 7) / 8 * 8;  // a whole number of tiles per XCD
-  hipLaunchKernelGGL((gdn_conv_prefill_kernel<span>), dim3((unsigned)(tiles + gate_blocks)), dim3(256), 0, stream_of(s), x, w,
-                     planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H, nspans, gate_blocks);
+  // the SiLU of the conv output: within float32 rounding (silu_tol) unless the process asked for the checker's bits
+  // (q27h_gdn_prefill_exact, read here when the launch is enqueued)
+  if (gdn_prefill_exact_mode())
+    hipLaunchKernelGGL((gdn_conv_prefill_kernel<span, false>), dim3((unsigned)(tiles + gate_blocks)), dim3(256), 0,
+                       stream_of(s), x, w, planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H,
+                       nspans, gate_blocks);
+  else
+    hipLaunchKernelGGL((gdn_conv_prefill_kernel<span, true>), dim3((unsigned)(tiles + gate_blocks)), dim3(256), 0,
+                       stream_of(s), x, w, planes, in_plane, y, C, M, n_norm_heads, eps, a, b, ssm_a, dt_bias, g, beta, H,
+                       nspans, gate_blocks);
   return check_launch("gdn_conv_prefill");
 }
 

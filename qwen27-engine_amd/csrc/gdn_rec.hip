@@ -201,6 +201,7 @@ constexpr int kChunkMinT = 128;
 static std::atomic<int> g_prefill_exact{0};
 
 extern "C" int q27h_gdn_prefill_exact(int on) { return g_prefill_exact.exchange(on ? 1 : 0); }
+bool q27h::gdn_prefill_exact_mode() { return g_prefill_exact.load(std::memory_order_relaxed) != 0; }
 
 extern "C" int q27h_gdn_step(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
                              float* planes, const int* in_plane, float* o, int H, int HK, int T, float scale, int snapshots,
@@ -212,7 +213,7 @@ extern "C" int q27h_gdn_step(const float* q, const float* k, const float* v, int
   if (!aligned16(q) || !aligned16(k) || !aligned16(planes))
     return fail(Q27H_ERR_ARG, "gdn_step: q, k and planes need 16-byte alignment");
   // the switch is read here, when the launch is enqueued: a graph captured under one setting keeps its path
-  if (flip && T >= kChunkMinT && !g_prefill_exact.load(std::memory_order_relaxed) &&
+  if (flip && T >= kChunkMinT && !gdn_prefill_exact_mode() &&
       !gdn_chunk_o_overlaps(q, k, v, stride, g, beta, planes, o, H, HK, T))
     return q27h_gdn_step_chunked(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, s);
   if (!flip && snapshots && T > 1)

@@ -39,17 +39,17 @@ enum RowMode { kPlain = 0, kAddPartial = 1, kAddBf16Recv = 2, kAddQ8Wire = 3 };
 constexpr int kGatedG = Q27H_GATED_G;
 constexpr int kLatencyRows = 64;  // row launches up to this many rows take the latency-bound kernel variants  // groups of 8 heads per workgroup in gated_rmsnorm_q8
 constexpr bool kRowNT = Q27H_NT_ROW, kSwigluNT = Q27H_NT_SWIGLU, kQuantNT = Q27H_NT_QUANT, kGatedNT = Q27H_NT_GATED;
+// Q27H_ROW_NT: 0 plain loads, 1 nontemporal loads in every row kernel, 2 nontemporal loads in the prefill-sized
+// (non-EXACT) residual-add kernels only
+template <bool NTL>
 __device__ __forceinline__ float4 ld4_row(const float* p) {
-#if Q27H_ROW_NT
-  return ld4_nt(p);
-#else
-  return ld4(p);
-#endif
+  if constexpr (NTL) return ld4_nt(p);
+  else return ld4(p);
 }
 
 // MODE kAddQ8Wire: x += dequant(own) + dequant(recv), two q8 wire rows (wown, wrecv: n int8 values, then n / qb fp16
 // scales per row; qb = 1 << qb_shift values per scale).
-template <int MODE, bool EXACT>
+template <int MODE, bool EXACT, bool NTL>
 __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x, const float* __restrict__ partial,
                                                           const uint16_t* __restrict__ recv, const float* __restrict__ w,
                                                           float eps, float* __restrict__ h, int8_t* __restrict__ xq,
@@ -76,12 +76,12 @@ __global__ void __launch_bounds__(256) row_norm_q8_kernel(float* __restrict__ x,
   uint16_t odb[NQ], rdb[NQ];
 #pragma unroll
   for (int k = 0; k < 5; k++) {
-    const float4 a = ld4_row(xr + off + k * 1024);
+    const float4 a = ld4_row<NTL>(xr + off + k * 1024);
     v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
   }
   if constexpr (MODE == kAddPartial || MODE == kAddBf16Recv) {
 #pragma unroll
-    for (int k = 0; k < 5; k++) pv4[k] = ld4_row(pr + off + k * 1024);
+    for (int k = 0; k < 5; k++) pv4[k] = ld4_row<NTL>(pr + off + k * 1024);
   }
   if constexpr (MODE == kAddBf16Recv) {
 #pragma unroll
@@ -375,8 +375,12 @@ int launch_rows(const char* fn, float* x, const float* partial, const uint16_t* 
   // (dynamic LDS of 32, 40 or 54 KB per workgroup) made no difference to the pass; 80 KB made it 8% slower. The
   // in-place x store right after the loads, before the reduction, is worth 140 us per pass against storing x after
   // it beside the q8_1 output (10.41-10.48 against 10.55-10.61 ms).
-  hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv, w, eps, h,
-                     xq, xd, xs, wown, wrecv, qb_shift);
+  if (Q27H_ROW_NT == 2 && MODE != kPlain && rows > kLatencyRows)
+    hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true, true>), dim3(rows), dim3(256), 0, stream_of(s), x, partial, recv,
+                       w, eps, h, xq, xd, xs, wown, wrecv, qb_shift);
+  else
+    hipLaunchKernelGGL((row_norm_q8_kernel<MODE, true, Q27H_ROW_NT == 1>), dim3(rows), dim3(256), 0, stream_of(s), x,
+                       partial, recv, w, eps, h, xq, xd, xs, wown, wrecv, qb_shift);
   return check_launch(fn);
 }
 

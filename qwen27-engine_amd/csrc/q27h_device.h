@@ -244,6 +244,27 @@ __device__ __forceinline__ void q27_silu_n(const float (&x)[N], float (&out)[N])
     for (int k = 0; k < N; k++) out[k] = q27_silu(x[k]);
   }
 }
+// silu within a few float32 ulps (not bit-exact): x * sigmoid(x) from e = 2^(-|x| log2 e) in (0, 1] on the hardware
+// exp2 (the product's rounding restored by one first-order term), the hardware reciprocal of 1 + e with one Newton
+// step, and x * e / (1 + e) for negative x. No overflow anywhere: e <= 1 and 1 <= 1 + e <= 2. Relative error below
+// 1e-6 for |x| <= 87; for x < -87 the value is a tiny negative number where the correctly rounded quotient
+// x / (1 + e^-x) is -0 or subnormal.
+__device__ __forceinline__ float silu_tol(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float t = ax * -1.44269502f;
+  const float lo = __builtin_fmaf(ax, -1.44269502f, -t) + ax * -1.925963e-8f;  // -|x| log2 e - t
+  float e = __builtin_amdgcn_exp2f(t);
+  e = __builtin_fmaf(e, lo * 0.693147181f, e);
+  const float d = 1.0f + e;
+  float r = __builtin_amdgcn_rcpf(d);
+  r = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+  return x * (x < 0.0f ? e * r : r);
+}
+template <int N>
+__device__ __forceinline__ void q27_silu_tol_n(const float (&x)[N], float (&out)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; k++) out[k] = silu_tol(x[k]);
+}
 __device__ __forceinline__ float q27_sigmoid(float x) { return 1.0f / (1.0f + q27_expf(-x)); }
 __device__ __forceinline__ float q27_softplus(float x) { return x > 20.0f ? x : q27_logf(1.0f + q27_expf(x)); }
 

@@ -22,6 +22,8 @@ inline bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
   return na && nb && x < y + nb && y < x + na;
 }
 
+// gdn_rec.hip: whether the process asked for the checker's bits on the GDN prefill path (q27h_gdn_prefill_exact).
+bool gdn_prefill_exact_mode();
 // gdn_chunk.hip: whether o shares memory with an input of the chunked delta-rule prefill (which it may not).
 bool gdn_chunk_o_overlaps(const float* q, const float* k, const float* v, int stride, const float* g, const float* beta,
                           const float* planes, const float* o, int H, int HK, int T);
