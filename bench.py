@@ -890,6 +890,8 @@ def main():
                     help="only the timed prefill steps (for rocprof counter runs): no breakdown, roofline, decode or CPU legs")
     ap.add_argument("--repack-only", action="store_true", help="only the qmat_upload repack of each weight type")
     ap.add_argument("--decode-only", action="store_true", help="only the decode verify pass (T = 4) graph")
+    ap.add_argument("--cfg45-only", action="store_true",
+                    help="only the configs[3] gathers and the configs[4] multimodal legs (for rocprof counter runs)")
     ap.add_argument("--isolated-only", action="store_true",
                     help="only the per-op isolated legs of the prefill pass (each op's launches back to back)")
     ap.add_argument("--gdn-only", action="store_true", help="only the delta-rule recurrence legs (for rocprof counter runs)")
@@ -910,6 +912,12 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}")
     if args.repack_only:
         print(json.dumps({"qmat_repack": bench_repack(q27, torch)}), flush=True)
+        return
+    if args.cfg45_only:
+        out = {"gathers_cfg4": bench_gathers(q27, torch)}
+        torch.cuda.empty_cache()
+        out["multimodal_cfg5"] = bench_multimodal(q27, torch)
+        print(json.dumps(out), flush=True)
         return
     if args.decode_only:
         decode_us, decode_ops = bench_decode_graph(q27, torch, args.graph_replays)
