@@ -480,11 +480,33 @@ __device__ __forceinline__ void load_chunk(Chunk<TYPE>& c, const Mat& m, size_t 
   }
 }
 
+// Types whose four-column, one-block-per-lane kernel parks the sums of rows 0-3 in LDS (dot_chunk's PARK). Measured
+// (us, 17408 x 5120 / 6144 x 5120, T = 4, against the sums in registers): IQ3_S 18.9 / 9.9-10.0 against 19.7-19.8 /
+// 10.1 (and no scratch), IQ2_XXS 18.3-18.6 / 9.3-9.5 against 18.9 / 9.6, IQ1_M 22.1-22.2 / 11.75 against 22.8-22.9 /
+// 11.8; Q6_K (21.2-21.5 against 20.0) and IQ4_XS (18.0 against 17.6) ran slower, Q2_K, IQ2_XS, IQ3_XXS and IQ2_S the
+// same within noise.
+constexpr bool parks_sums(int type) { return type == kIQ3S || type == kIQ2XXS || type == kIQ1M; }
+
+// acc[r * NC + c] += t, or with PARK and r < 4 the finished sum to the lane's LDS slot (see dot_chunk).
+template <bool PARK, int NC>
+__device__ __forceinline__ void acc_add(float (&acc)[8 * NC], float* park, int r, int c, float t) {
+  if constexpr (PARK) {
+    if (r < 4) {
+      park[(r * NC + c) * 256] = acc[r * NC + c] + t;
+      return;
+    }
+  }
+  acc[r * NC + c] += t;
+}
+
 // acc[r * NC + c] += t(row r, column c) for one chunk; u[c] = the 32 int8 activations of column c, dy[c] its scale.
-template <int TYPE, int NC>
+// PARK: the sums of rows 0-3 go to LDS (park[value * 256], the lane's own slots) as soon as the row is done, instead
+// of staying in registers for the whole chunk; used where a lane has one chunk, so the parked value is the
+// accumulator's final one.
+template <int TYPE, int NC, bool PARK = false>
 __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[NC][8], const float (&dy)[NC],
                                           const uint32_t* __restrict__ lut, const uint32_t (&kv)[4],
-                                          float (&acc)[8 * NC]) {
+                                          float (&acc)[8 * NC], float* park = nullptr) {
   const uint32_t* w = ch.w;
   if constexpr (TYPE == kQ4K) {
     // (the min term's (float)(s8 * m) equals (float)s8 * (float)m exactly, |s8 * m| < 2^24; that form, one multiply
@@ -514,7 +536,8 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const float d = half_lo(w[36 + r]), dmin = half_hi(w[36 + r]);
 #pragma unroll
       for (int c = 0; c < NC; c++)
-        acc[r * NC + c] += d * (dy[c] * (float)mul24(sumi[c], sc)) - dmin * (dy[c] * (float)mul24(s8[c], mn));
+        acc_add<PARK, NC>(acc, park, r, c,
+                          d * (dy[c] * (float)mul24(sumi[c], sc)) - dmin * (dy[c] * (float)mul24(s8[c], mn)));
     }
   } else if constexpr (TYPE == kQ6K) {
     int s8a[NC], s8b[NC];  // activation sums of the two 16-weight halves (the -32 offset of the quants)
@@ -552,7 +575,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
 #pragma unroll
       for (int c = 0; c < NC; c++) {
         const int si = mul24(sa[c] - 32 * s8a[c], sc0) + mul24(sb[c] - 32 * s8b[c], sc1);
-        acc[r * NC + c] += d * (dy[c] * (float)si);
+        acc_add<PARK, NC>(acc, park, r, c, d * (dy[c] * (float)si));
       }
     }
   } else if constexpr (TYPE == kIQ3S) {
@@ -592,7 +615,10 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const int mul = 1 + 2 * (int)((w[26] >> (4 * r)) & 0xF);
       const float d = (r & 1) ? half_hi(w[27 + r / 2]) : half_lo(w[27 + r / 2]);
 #pragma unroll
-      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)mul24(sumi[c], mul);
+      for (int c = 0; c < NC; c++) {
+        const float t = (d * dy[c]) * (float)mul24(sumi[c], mul);
+        acc_add<PARK, NC>(acc, park, r, c, t);
+      }
     }
   } else if constexpr (TYPE == kIQ4XS) {
 #pragma unroll
@@ -610,7 +636,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const int ls = (int)(int8_t)((w[32 + r / 4] >> (8 * (r & 3))) & 0xFF);
       const float d = (r & 1) ? half_hi(w[34 + r / 2]) : half_lo(w[34 + r / 2]);
 #pragma unroll
-      for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)mul24(sumi[c], ls);
+      for (int c = 0; c < NC; c++) acc_add<PARK, NC>(acc, park, r, c, (d * dy[c]) * (float)mul24(sumi[c], ls));
     }
   } else if constexpr (TYPE == kQ2K) {
     int s8a[NC], s8b[NC];  // activation sums of the two 16-weight halves (the min terms multiply them)
@@ -646,7 +672,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       for (int c = 0; c < NC; c++) {
         const int sd = mul24(sa[c], g0 & 0xF) + mul24(sb[c], g1 & 0xF);
         const int smn = mul24(s8a[c], g0 >> 4) + mul24(s8b[c], g1 >> 4);
-        acc[r * NC + c] += d * (dy[c] * (float)sd) - dmin * (dy[c] * (float)smn);
+        acc_add<PARK, NC>(acc, park, r, c, d * (dy[c] * (float)sd) - dmin * (dy[c] * (float)smn));
       }
     }
   } else if constexpr (TYPE == kIQ2XXS || TYPE == kIQ2XS || TYPE == kIQ2S) {
@@ -689,7 +715,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
         const int ls = (int)((w[2 * r + 1] >> 27) | 1);
         const float d = (r & 1) ? half_hi(w[16 + r / 2]) : half_lo(w[16 + r / 2]);
 #pragma unroll
-        for (int c = 0; c < NC; c++) acc[r * NC + c] += (d * dy[c]) * (float)(mul24(s0[c], ls) / 8);
+        for (int c = 0; c < NC; c++) acc_add<PARK, NC>(acc, park, r, c, (d * dy[c]) * (float)(mul24(s0[c], ls) / 8));
       } else {
         const uint32_t lsb = TYPE == kIQ2XS ? (w[16 + r / 4] >> (8 * (r & 3))) & 0xFF : (w[18 + r / 4] >> (8 * (r & 3))) & 0xFF;
         const int ls0 = (int)(lsb & 0xF), ls1 = (int)(lsb >> 4);
@@ -698,7 +724,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
 #pragma unroll
         for (int c = 0; c < NC; c++) {
           const int si = (mul24(s0[c], ls0) + mul24(s1[c], ls1) + (s0[c] + s1[c]) / 2) / 4;
-          acc[r * NC + c] += (d * dy[c]) * (float)si;
+          acc_add<PARK, NC>(acc, park, r, c, (d * dy[c]) * (float)si);
         }
       }
     }
@@ -728,7 +754,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
 #pragma unroll
       for (int c = 0; c < NC; c++) {
         const int si = (mul24(ls, sumi[c]) + sumi[c] / 2) / 2;
-        acc[r * NC + c] += (d * dy[c]) * (float)si;
+        acc_add<PARK, NC>(acc, park, r, c, (d * dy[c]) * (float)si);
       }
     }
   } else if constexpr (TYPE == kIQ1M) {
@@ -766,7 +792,7 @@ __device__ __forceinline__ void dot_chunk(const Chunk<TYPE>& ch, const int (&u)[
       const float d = (r & 1) ? half_hi(w[14 + r / 2]) : half_lo(w[14 + r / 2]);
 #pragma unroll
       for (int c = 0; c < NC; c++)
-        acc[r * NC + c] += (d * dy[c]) * ((((float)si[c][0] + sf[c][0]) * sc0) + (((float)si[c][1] + sf[c][1]) * sc1));
+        acc_add<PARK, NC>(acc, park, r, c, (d * dy[c]) * ((((float)si[c][0] + sf[c][0]) * sc0) + (((float)si[c][1] + sf[c][1]) * sc1)));
     }
   }
 }
@@ -894,7 +920,19 @@ __device__ __forceinline__ void qgemv_body(Mat m, const int8_t* __restrict__ xq,
         dy[c] = xd[(size_t)c * (K / 32) + bb * 8 + s];
       }
     };
-    if constexpr (ONE) {
+    if constexpr (ONE && !FUSED && NC == 4 && parks_sums(TYPE)) {
+      // four columns: the 16 sums of rows 0-3 parked in LDS row by row keep the chunk's decode in fewer VGPRs (IQ3_S:
+      // 90 instead of a 128-VGPR cap and a 12-byte spill to scratch); the values and their order are unchanged
+      __shared__ float park[4 * NC][256];
+      if (b < m.nb) {
+        load_chunk<TYPE, NTP>(ca, m, (size_t)tile, b, s);
+        load_x(b);
+        dot_chunk<TYPE, NC, true>(ca, u, dy, lut, kv, acc, &park[0][threadIdx.x]);
+        asm volatile("" ::: "memory");  // the sums come back from LDS, not from registers the compiler kept
+#pragma unroll
+        for (int i = 0; i < 4 * NC; i++) acc[i] = park[i][threadIdx.x];
+      }
+    } else if constexpr (ONE) {
       if (b < m.nb) {
         load_chunk<TYPE, NTP>(ca, m, (size_t)tile, b, s);
         load_x(b);
@@ -949,10 +987,8 @@ __device__ __forceinline__ void qgemv_body(Mat m, const int8_t* __restrict__ xq,
 // Q4_K with four columns keep the prefetching kernel). The additions are the same, so the results are identical.
 // Its wide pieces are always read with nontemporal loads: ordinary loads at K = 17408 measured 2-5% slower (Q6_K T = 1
 // 13.7 -> 14.3 us), the opposite of the prefetching kernel.
-// IQ3_S with four columns needs a few more than 128 VGPRs here and spills 12 bytes per lane (about 2 MB of scratch
-// traffic per 17408 x 5120 launch); both ways of avoiding the spill measured slower (us, 17408 x 5120 / 5120 x 17408,
-// T = 4): 3 waves per SIMD for that instantiation 21.3 / 20.4 against 19.8 / 20.5, and the row's codebook reads in two
-// halves 20.5 / 23.9 against 19.7 / 20.2.
+// IQ3_S with four columns needed a few more than 128 VGPRs here and spilled 12 bytes per lane to scratch (about 2 MB
+// of scratch traffic per 17408 x 5120 launch) until the sums of half the rows were parked in LDS (parks_sums).
 #ifndef Q27H_QG_WPE_ONE
 #define Q27H_QG_WPE_ONE 4
 #endif
