@@ -16,6 +16,11 @@ against the file.
 - l2norm_heads (src/ops.cu:437-447): heads of 128 from treepins.l2_lanes / l2_korder, y = (x * scale) * post with
   scale = 1 / sqrtf(sum / 128 + eps / 128), post = 1 / sqrtf(128).
 - get_rows_q8_0 (src/ops.cu:343-375 with ggml's Q8_0 block: fp16 d, 32 int8): y = fp16(d) * q, exact in float32.
+- attn_prep (src/ops.cu:587-654) with every IMRoPE position 0 (rope3 all zero), so every rotary angle is 0 and the
+  rotation is the identity (sin 0 = 0 and cos 0 = 1 exactly): qn = (scale * q) * q_norm per head of 256, with scale =
+  1 / sqrtf(sum / 256 + eps) from the hand-derived sum of treepins.head_warps(256) (token 0) or the exact sum of
+  nonzero small integers (tokens 1-3); the q8_0 K / V cache rows of (scale * k) * k_norm and of v: per 32 values d =
+  amax / 127, q = roundf(y * (1 / d)), fp16(d) in the scale area after the int8 area (src/attn.cu:890-892).
 
 Run from the repository root: python tests/golden/make_golden.py
 """
@@ -113,6 +118,60 @@ def q8_0_table():
     return tab.reshape(-1), ids, y.reshape(-1)
 
 
+def q8_0_rows(y):
+    """The q8_0 cache rule over blocks of 32: q = roundf(y * (1 / d)), d = amax / 127; returns int8 and fp16 bits."""
+    b = np.ascontiguousarray(y, np.float32).reshape(-1, 32)
+    d = (np.abs(b).max(1) / f32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(d != 0, f32(1) / d, f32(0)).astype(np.float32)
+    q = round_half_away((b * inv[:, None]).astype(np.float32)).astype(np.int8)
+    return q.reshape(-1), d.astype(np.float16).view(np.uint16)
+
+
+def attn_case():
+    r = np.random.default_rng(20264)
+    Tn, nqh, nkvh, n_ctx, pos0 = 4, 24, 4, 16, 7
+    good, bad = tp.HEAD_WARPS_SUM[256], tp.HEAD_WARPS_SEQ[256]
+    eps = tp.eps_separating(good, bad, 256)
+    tree = tp.head_warps(256)
+
+    def heads(n):
+        h = r.integers(1, 9, (Tn, n, 256)) * np.where(r.random((Tn, n, 256)) < 0.5, -1, 1)
+        h = h.astype(np.float32)
+        h[0, :] = tree
+        return h
+
+    q, k = heads(nqh), heads(nkvh)
+    v = (r.standard_normal((Tn, nkvh, 256)) * 2).astype(np.float32)
+    qw = (r.standard_normal(256) * 0.1 + 1).astype(np.float32)
+    kw = (r.standard_normal(256) * 0.1 + 1).astype(np.float32)
+    qg = np.zeros((Tn, nqh, 512), np.float32)
+    qg[:, :, :256] = q
+    qg[:, :, 256:] = r.integers(-99, 100, (Tn, nqh, 256)).astype(np.float32)  # the gate half, not read
+
+    def normed(x, w):
+        sums = np.sum(x.astype(np.float64) ** 2, axis=-1)
+        sums[0, :] = good  # token 0: the reference tree's sum, derived by hand
+        sc = np.vectorize(lambda t: tp.row_scale(t, 256, eps))(sums).astype(np.float32)
+        return (sc[..., None] * x) * w
+
+    qn = normed(q, qw)
+    kn = normed(k, kw)
+    kc = np.zeros(nkvh * n_ctx * 272, np.uint8)
+    vc = np.zeros(nkvh * n_ctx * 272, np.uint8)
+    so = nkvh * n_ctx * 256
+    for cache, src in ((kc, kn), (vc, v)):
+        for t in range(Tn):
+            for h in range(nkvh):
+                row = h * n_ctx + pos0 + t
+                qq, dd = q8_0_rows(src[t, h])
+                cache[row * 256:(row + 1) * 256] = qq.view(np.uint8)
+                cache[so + row * 16:so + (row + 1) * 16] = dd.view(np.uint8)
+    return {"att_qg": qg.reshape(-1), "att_k": k.reshape(-1), "att_v": v.reshape(-1), "att_qw": qw, "att_kw": kw,
+            "att_eps": np.float32(eps), "att_pos0": np.int32(pos0), "att_nctx": np.int32(n_ctx),
+            "att_rope3": np.zeros((Tn, 3), np.int32), "att_qn": qn.reshape(-1), "att_kc": kc, "att_vc": vc}
+
+
 def main():
     out = {}
     x = q8_blocks()
@@ -124,6 +183,7 @@ def main():
     for i, (xh, e, y) in enumerate(l2_cases()):
         out[f"l2{i}_x"], out[f"l2{i}_eps"], out[f"l2{i}_y"] = xh, np.float32(e), y
     out["q80_table"], out["q80_ids"], out["q80_y"] = q8_0_table()
+    out.update(attn_case())
     path = os.path.join(HERE, "known_answers.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path}: {len(out)} arrays")

@@ -11,6 +11,7 @@ from conftest import assert_bits_equal
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "known_answers.npz")
 E = 5120
+THETA = float(np.float32(1e7) ** np.float32(-2.0 / 64))  # any theta: every angle is 0 in the attn_prep case
 
 
 @pytest.fixture(scope="module")
@@ -70,3 +71,13 @@ def test_l2norm_golden(oracle, G, i):
 def test_get_rows_q8_0_golden(oracle, G):
     y = oracle.get_rows("q8_0", G["q80_table"], 34 * (E // 32), G["q80_ids"], E)
     assert_bits_equal(y, G["q80_y"], "q8_0 rows")
+
+
+def test_attn_prep_golden(oracle, G):
+    nb = G["att_kc"].size
+    kc, vc = np.zeros(nb, np.uint8), np.zeros(nb, np.uint8)
+    qn = oracle.attn_prep(G["att_qg"], G["att_k"], G["att_v"], G["att_qw"], G["att_kw"], kc, vc, int(G["att_pos0"]), 4,
+                          float(G["att_eps"]), THETA, 24, 4, int(G["att_nctx"]), True, G["att_rope3"])
+    assert_bits_equal(qn, G["att_qn"], "qn")
+    assert_bits_equal(kc, G["att_kc"], "k cache")
+    assert_bits_equal(vc, G["att_vc"], "v cache")

@@ -11,6 +11,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "known_answers.npz")
 E = 5120
+THETA = float(np.float32(1e7) ** np.float32(-2.0 / 64))  # any theta: every angle is 0 in the attn_prep case
 
 
 def say(msg):
@@ -96,3 +97,32 @@ def test_get_rows_q8_0_golden_on_gpu(q27, T, G, reps):
     y = T.empty(ids.size * E)
     q27.ops.get_rows_q8_0(T.up(G["q80_table"]), 34 * (E // 32), T.up(ids.astype(np.int32)), ids.size, y, E)
     same(T.down(y), np.tile(G["q80_y"], reps), "q8_0 rows")
+
+
+@pytest.mark.parametrize("reps", [1, 128])
+def test_attn_prep_golden_on_gpu(q27, T, G, reps):
+    """reps = 1: the 4-token decode form; reps = 128: the 4 tokens repeated to 512 (one workgroup per token), the
+    cache rows of token t being those of token t % 4 at row pos0 + t."""
+    import torch
+
+    say(f"attn_prep golden reps={reps}")
+    nqh, nkvh, pos0, nctx0 = 24, 4, int(G["att_pos0"]), int(G["att_nctx"])
+    Tn = 4 * reps
+    nctx = nctx0 if reps == 1 else 1024
+    nb = nkvh * nctx * 272
+    kc, vc = T.empty(nb, torch.uint8), T.empty(nb, torch.uint8)
+    qn = T.empty(Tn * nqh * 256)
+    q27.ops.attn_prep(T.up(np.tile(G["att_qg"], reps)), T.up(np.tile(G["att_k"], reps)), T.up(np.tile(G["att_v"], reps)),
+                      T.up(G["att_qw"]), T.up(G["att_kw"]), qn, kc, vc, T.up(np.array([pos0], np.int32)), Tn,
+                      float(G["att_eps"]), THETA, nqh, nkvh, nctx, True, None, None, 0,
+                      T.up(np.zeros((Tn, 3), np.int32)), None)
+    same(T.down(qn), np.tile(G["att_qn"], reps), "qn")
+    so0, so = nkvh * nctx0 * 256, nkvh * nctx * 256
+    for got, gold, what in ((kc, G["att_kc"], "k cache"), (vc, G["att_vc"], "v cache")):
+        want = np.zeros(nb, np.uint8)
+        for h in range(nkvh):
+            for t in range(Tn):
+                r0, r = h * nctx0 + pos0 + t % 4, h * nctx + pos0 + t
+                want[r * 256:(r + 1) * 256] = gold[r0 * 256:(r0 + 1) * 256]
+                want[so + r * 16:so + (r + 1) * 16] = gold[so0 + r0 * 16:so0 + (r0 + 1) * 16]
+        same(T.down(got), want, what)
