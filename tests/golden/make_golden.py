@@ -172,7 +172,8 @@ def attn_case():
             "att_rope3": np.zeros((Tn, 3), np.int32), "att_qn": qn.reshape(-1), "att_kc": kc, "att_vc": vc}
 
 
-def main():
+def build():
+    """Every array of the file, by name."""
     out = {}
     x = q8_blocks()
     out["q8_x"] = x
@@ -184,6 +185,11 @@ def main():
         out[f"l2{i}_x"], out[f"l2{i}_eps"], out[f"l2{i}_y"] = xh, np.float32(e), y
     out["q80_table"], out["q80_ids"], out["q80_y"] = q8_0_table()
     out.update(attn_case())
+    return out
+
+
+def main():
+    out = build()
     path = os.path.join(HERE, "known_answers.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path}: {len(out)} arrays")
