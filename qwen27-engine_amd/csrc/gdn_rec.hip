@@ -35,6 +35,17 @@ constexpr int kCols = Q27H_GDN_COLS;    // columns per workgroup
 #define Q27H_GDN_GT 32
 #endif
 constexpr int kGT = Q27H_GDN_GT;        // tokens staged per LDS round
+#ifndef Q27H_GDN_DEC_COLS
+#define Q27H_GDN_DEC_COLS 32
+#endif
+// Decode (T <= 4 tokens, graph of 64 steps, 48 heads, snapshots): 5.28 against 5.55 us for the prefill form (32
+// columns, 32-token staging, plain stores): a 4-token staging round (5.47 us) and nontemporal state-plane stores
+// (the planes are next read a whole decode step later). 8 or 16 columns per workgroup (all CUs busy) ran 5.39-5.48 us.
+#ifndef Q27H_GDN_SNAP_NT
+#define Q27H_GDN_SNAP_NT 1
+#endif
+constexpr bool kSnapNT = Q27H_GDN_SNAP_NT;  // nontemporal stores of the state planes
+constexpr int kDecCols = Q27H_GDN_DEC_COLS;  // columns per workgroup of a decode step (T <= 4, one staging round)
 
 // Sum over the parts of a column (PARTS consecutive lanes): xor butterfly with masks 1, 2, 7 (, 8), which span the
 // lane bits of a part index and are all DPP moves (quad_perm, row_half_mirror, row_ror:8). Each step adds a lane
@@ -48,11 +59,11 @@ __device__ __forceinline__ float parts_sum(float v) {
   return v;
 }
 
-// One staging round in registers: q / k of kGT tokens as float4 pieces (32 per token and vector), v of the
-// workgroup's kCols columns, g and beta.
-template <int THREADS>
+// One staging round in registers: q / k of GT tokens as float4 pieces (32 per token and vector), v of the
+// workgroup's COLS columns, g and beta (the counts round up; pieces past the round are skipped by their guards).
+template <int THREADS, int GT, int COLS>
 struct Stage {
-  static constexpr int NQ = kGT * 32 / THREADS, NV = kGT * kCols / THREADS;
+  static constexpr int NQ = (GT * 32 + THREADS - 1) / THREADS, NV = (GT * COLS + THREADS - 1) / THREADS;
   float4 q[NQ], k[NQ];
   float v[NV];
   float g, b;
@@ -62,23 +73,24 @@ struct Stage {
 #define Q27H_GDN_UNROLL 32  // full rounds fully unrolled: 509 us for 2048 tokens, 535 us with 1, 544 us with 4
 #endif
 
-// SNAP: decode with per-token snapshots (plane t after token t); otherwise only the final state is written.
-template <int PARTS, bool SNAP>
-__global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __restrict__ q, const float* __restrict__ k,
+// SNAP: decode with per-token snapshots (plane t after token t); otherwise only the final state is written. COLS
+// columns per workgroup, GT tokens per staging round; the arithmetic of a column does not depend on either.
+template <int PARTS, bool SNAP, int COLS = kCols, int GT = kGT>
+__global__ void __launch_bounds__(COLS * PARTS) gdn_rec_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                                 const float* __restrict__ v, int stride,
                                                                 const float* __restrict__ g, const float* __restrict__ beta,
                                                                 float* __restrict__ planes, const int* __restrict__ in_plane,
                                                                 float* __restrict__ o, int H, int HK, int T, float scale,
                                                                 int flip) {
-  constexpr int EPL = 128 / PARTS, PAD = EPL + 4, ROW = PARTS * PAD, THREADS = kCols * PARTS;
+  constexpr int EPL = 128 / PARTS, PAD = EPL + 4, ROW = PARTS * PAD, THREADS = COLS * PARTS;
   // q / k rows padded by 4 floats per part (the parts' float4 reads fall in different banks); two buffers, the
   // next round is loaded while the current one is consumed
-  __shared__ __align__(16) float sq[2][kGT][ROW];
-  __shared__ __align__(16) float sk[2][kGT][ROW];
-  __shared__ float sv[2][kGT][kCols];
-  __shared__ float sg[2][kGT], sb[2][kGT];
+  __shared__ __align__(16) float sq[2][GT][ROW];
+  __shared__ __align__(16) float sk[2][GT][ROW];
+  __shared__ float sv[2][GT][COLS];
+  __shared__ float sg[2][GT], sb[2][GT];
   const int h = blockIdx.x, kh = h % HK;
-  const int tid = threadIdx.x, p = tid & (PARTS - 1), cl = tid / PARTS, col = blockIdx.y * kCols + cl;
+  const int tid = threadIdx.x, p = tid & (PARTS - 1), cl = tid / PARTS, col = blockIdx.y * COLS + cl;
   const size_t plane_sz = (size_t)H * 128 * 128;
   const int pin = *in_plane;
   const size_t soff = ((size_t)h * 128 + col) * 128 + EPL * p;
@@ -91,9 +103,9 @@ __global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __r
       s[i] = a.x; s[i + 1] = a.y; s[i + 2] = a.z; s[i + 3] = a.w;
     }
   }
-  using St = Stage<THREADS>;
+  using St = Stage<THREADS, GT, COLS>;
   auto load = [&](St& r, int t0) {
-    const int nt = min(kGT, T - t0);
+    const int nt = min(GT, T - t0);
 #pragma unroll
     for (int j = 0; j < St::NQ; j++) {
       const int i = tid + j * THREADS, t = i >> 5, e4 = (i & 31) * 4;
@@ -104,8 +116,8 @@ __global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __r
     }
 #pragma unroll
     for (int j = 0; j < St::NV; j++) {
-      const int i = tid + j * THREADS, t = i / kCols, c = i % kCols;
-      if (t < nt) r.v[j] = v[(size_t)(t0 + t) * stride + h * 128 + blockIdx.y * kCols + c];
+      const int i = tid + j * THREADS, t = i / COLS, c = i % COLS;
+      if (t < nt) r.v[j] = v[(size_t)(t0 + t) * stride + h * 128 + blockIdx.y * COLS + c];
     }
     if (tid < nt) {
       r.g = g[(size_t)(t0 + tid) * H + h];
@@ -113,7 +125,7 @@ __global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __r
     }
   };
   auto store = [&](const St& r, int buf, int t0) {
-    const int nt = min(kGT, T - t0);
+    const int nt = min(GT, T - t0);
 #pragma unroll
     for (int j = 0; j < St::NQ; j++) {
       const int i = tid + j * THREADS, t = i >> 5, e4 = (i & 31) * 4, pe = (e4 / EPL) * PAD + e4 % EPL;
@@ -124,7 +136,7 @@ __global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __r
     }
 #pragma unroll
     for (int j = 0; j < St::NV; j++) {
-      const int i = tid + j * THREADS, t = i / kCols, c = i % kCols;
+      const int i = tid + j * THREADS, t = i / COLS, c = i % COLS;
       if (t < nt) sv[buf][t][c] = r.v[j];
     }
     if (tid < nt) {
@@ -139,11 +151,11 @@ __global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __r
     store(r, 0, 0);
   }
   __syncthreads();
-  for (int t0 = 0, buf = 0; t0 < T; t0 += kGT, buf ^= 1) {
-    const int nt = min(kGT, T - t0);
-    const bool more = t0 + kGT < T;
+  for (int t0 = 0, buf = 0; t0 < T; t0 += GT, buf ^= 1) {
+    const int nt = min(GT, T - t0);
+    const bool more = t0 + GT < T;
     St r;
-    if (more) load(r, t0 + kGT);  // in flight during the tokens below
+    if (more) load(r, t0 + GT);  // in flight during the tokens below
     auto step = [&](int tt) {
       float kr[EPL], qr[EPL];
 #pragma unroll
@@ -171,21 +183,21 @@ __global__ void __launch_bounds__(kCols * PARTS) gdn_rec_kernel(const float* __r
       if (SNAP && t < T - 1) {
         float* W = planes + (size_t)t * plane_sz + soff;
 #pragma unroll
-        for (int i = 0; i < EPL; i += 4) st4(W + i, s[i], s[i + 1], s[i + 2], s[i + 3]);
+        for (int i = 0; i < EPL; i += 4) st4<kSnapNT>(W + i, s[i], s[i + 1], s[i + 2], s[i + 3]);
       }
     };
-    if (nt == kGT) {
+    if (nt == GT) {
 #pragma unroll Q27H_GDN_UNROLL
-      for (int tt = 0; tt < kGT; tt++) step(tt);
+      for (int tt = 0; tt < GT; tt++) step(tt);
     } else {
       for (int tt = 0; tt < nt; tt++) step(tt);
     }
-    if (more) store(r, buf ^ 1, t0 + kGT);
+    if (more) store(r, buf ^ 1, t0 + GT);
     __syncthreads();
   }
   float* W = planes + (size_t)out_plane * plane_sz + soff;
 #pragma unroll
-  for (int i = 0; i < EPL; i += 4) st4(W + i, s[i], s[i + 1], s[i + 2], s[i + 3]);
+  for (int i = 0; i < EPL; i += 4) st4<kSnapNT>(W + i, s[i], s[i + 1], s[i + 2], s[i + 3]);
 }
 
 }  // namespace
@@ -217,8 +229,11 @@ extern "C" int q27h_gdn_step(const float* q, const float* k, const float* v, int
       !gdn_chunk_o_overlaps(q, k, v, stride, g, beta, planes, o, H, HK, T))
     return q27h_gdn_step_chunked(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, s);
   if (!flip && snapshots && T > 1)
-    hipLaunchKernelGGL((gdn_rec_kernel<kParts, true>), dim3(H, 128 / kCols), dim3(kCols * kParts), 0, stream_of(s), q, k,
-                       v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, 0);
+    hipLaunchKernelGGL((gdn_rec_kernel<kParts, true, kDecCols, 4>), dim3(H, 128 / kDecCols), dim3(kDecCols * kParts), 0,
+                       stream_of(s), q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, 0);
+  else if (!flip)
+    hipLaunchKernelGGL((gdn_rec_kernel<kParts, false, kDecCols, 4>), dim3(H, 128 / kDecCols), dim3(kDecCols * kParts), 0,
+                       stream_of(s), q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, 0);
   else
     hipLaunchKernelGGL((gdn_rec_kernel<kParts, false>), dim3(H, 128 / kCols), dim3(kCols * kParts), 0, stream_of(s), q, k,
                        v, stride, g, beta, planes, in_plane, o, H, HK, T, scale, flip);
