@@ -718,6 +718,38 @@ def bench_repack(q27, torch, N=17408, K=5120):
     return out
 
 
+def bench_bf16_pair(q27, torch, N=HV, K=E):
+    """gemv_bf16_pair (src/ops.h:24-26), the decode alpha / beta projections: ya = Wa x, yb = Wb x for two bf16 [48][5120]
+    matrices at T = 1 and 4 tokens. `graph`: launches replayed from one HIP graph on one weight pair (decode-sized,
+    as in a decode step's graph; the 0.98 MB pair stays in the caches); `cold`: a graph whose nodes walk 320 weight
+    pairs (315 MB, more than the 256 MB MALL), as each GDN layer of a decode step reads its own. GB/s of the weights,
+    x and y per launch."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(37)
+    sets = 320
+    W = [(torch.randint(0, 65536, (N * K,), dtype=torch.int32, device=dev, generator=g).to(torch.int16),
+          torch.randint(0, 65536, (N * K,), dtype=torch.int32, device=dev, generator=g).to(torch.int16)) for _ in range(sets)]
+    for wa, wb in W:  # finite bf16 weights: clear the top exponent bit
+        wa &= 0x3FFF
+        wb &= 0x3FFF
+    out = {}
+    for T in (1, 4):
+        x = torch.randn(T * K, device=dev, generator=g)
+        ya, yb = torch.empty(T * N, device=dev), torch.empty(T * N, device=dev)
+        b = 2 * N * K * 2 + T * K * 4 + 2 * T * N * 4
+        us_g = time_graph(torch, lambda: q27.ops.gemv_bf16_pair(W[0][0], W[0][1], x, ya, yb, N, K, T), 200)
+        it = iter(range(1 << 30))  # the graph's nodes walk the weight pairs
+        us_c = time_graph(torch, lambda: (lambda i: q27.ops.gemv_bf16_pair(W[i % sets][0], W[i % sets][1], x, ya, yb, N,
+                                                                           K, T))(next(it)), sets)
+        out[f"T{T}"] = {"graph_us": round(us_g, 2), "cold_us": round(us_c, 2), "cold_GBps": round(b / us_c / 1e3, 1),
+                        "MB": round(b / 1e6, 2)}
+        log(f"  gemv_bf16_pair T={T}: {us_g:.2f} us in a graph, {us_c:.2f} us cold ({b / us_c / 1e3:.0f} GB/s)")
+    del W
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_wire(q27, torch, M=2048):
     """The two-card wire formats at the prefill batch (src/prefill.cu:338-406) on one GPU: to_q8_wire with carried
     error feedback, add_norm_rows_q8 (h = null, xs) and to_bf16 of [M][5120], both q8 widths. Three buffer sets
@@ -895,6 +927,7 @@ def main():
     ap.add_argument("--isolated-only", action="store_true",
                     help="only the per-op isolated legs of the prefill pass (each op's launches back to back)")
     ap.add_argument("--gdn-only", action="store_true", help="only the delta-rule recurrence legs (for rocprof counter runs)")
+    ap.add_argument("--wire-only", action="store_true", help="only the gemv_bf16_pair and two-card wire-format legs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the fused-op path has no multi-GPU form in this build "
@@ -925,6 +958,10 @@ def main():
         return
     if args.gdn_only:
         print(json.dumps({"gdn_recurrence": bench_gdn(q27, torch)}), flush=True)
+        return
+    if args.wire_only:
+        print(json.dumps({"gemv_bf16_pair": bench_bf16_pair(q27, torch), "wire_formats": bench_wire(q27, torch)}),
+              flush=True)
         return
 
     # ---- prefill pass (the step)
@@ -1047,6 +1084,8 @@ def main():
     torch.cuda.empty_cache()
     fused_gemv = bench_fused_gemv(q27, torch)
     gdn_rec = bench_gdn(q27, torch)
+    pair = bench_bf16_pair(q27, torch)
+    wire = bench_wire(q27, torch)
     upload = bench_upload(q27, torch)
     repack = bench_repack(q27, torch)
 
@@ -1102,6 +1141,8 @@ def main():
         "decode_gemv": gemv,
         "decode_quantize_gemv_fused": fused_gemv,
         "gdn_recurrence": gdn_rec,
+        "gemv_bf16_pair": pair,
+        "wire_formats": wire,
         "gguf_upload": upload,
         "qmat_repack": repack,
         "roofline": roofline,

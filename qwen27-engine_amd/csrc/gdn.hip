@@ -379,6 +379,7 @@ namespace {
 // (one 16-byte load of weights per step) and the warp butterfly is lane xor 7, 2, 1 plus the lane's own pairs; the
 // 8 warp sums live in the 8 lane groups and meet through lane xor 32, 16, 8 (the second butterfly's xor 4, 2, 1;
 // its xor 16 and 8 only add the zero entries).
+constexpr int kPairU = 10;  // steps of 512 weights in flight per lane
 __global__ void __launch_bounds__(256) gemv_bf16_pair_kernel(const uint16_t* __restrict__ Wa, const uint16_t* __restrict__ Wb,
                                                              const float* __restrict__ x, float* __restrict__ ya,
                                                              float* __restrict__ yb, int N, int K, int T) {
@@ -390,15 +391,32 @@ __global__ void __launch_bounds__(256) gemv_bf16_pair_kernel(const uint16_t* __r
   const float* xt = x + (size_t)t * K;
   const int k0 = 2 * (32 * (l >> 3) + 4 * quad_of_lane(l & 7));
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int k = k0; k < K; k += 512) {
-    const uint4 wv = *(const uint4*)(w + k);
-    const float4 xa = ld4(xt + k), xb = ld4(xt + k + 4);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
-    const float xx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  // kPairU steps of 512 weights (all of a 5120-wide row) are requested before the first is used, then added in k
+  // order: weights from HBM cost one memory round trip per batch instead of one per step. 48 x 5120, graph of 320
+  // launches over distinct weight pairs: 7.13 -> 4.01 us (T = 1), 6.85 -> 3.98 us (T = 4); one cached pair 3.20 ->
+  // 3.02 us. The sums and their order are unchanged.
+  for (int kb = k0; kb < K; kb += 512 * kPairU) {
+    uint4 wv[kPairU];
+    float4 xa[kPairU], xb[kPairU];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const float w0 = bf16_to_f((uint16_t)(ww[c] & 0xffff)), w1 = bf16_to_f((uint16_t)(ww[c] >> 16));
-      acc[c] = acc[c] + (w0 * xx[2 * c] + w1 * xx[2 * c + 1]);
+    for (int u = 0; u < kPairU; u++) {
+      const int k = kb + 512 * u;
+      if (k < K) {
+        wv[u] = *(const uint4*)(w + k);
+        xa[u] = ld4(xt + k);
+        xb[u] = ld4(xt + k + 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kPairU; u++) {
+      if (kb + 512 * u >= K) break;
+      const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+      const float xx[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float w0 = bf16_to_f((uint16_t)(ww[c] & 0xffff)), w1 = bf16_to_f((uint16_t)(ww[c] >> 16));
+        acc[c] = acc[c] + (w0 * xx[2 * c] + w1 * xx[2 * c + 1]);
+      }
     }
   }
   float v = vwarp_sum4(acc);
