@@ -512,7 +512,9 @@ def bench_gemv(q27, torch):
     """Decode GEMV (the consumer of the q8_1 activations, src/qgemv.cu): per weight type and model shape, us per
     launch and GB/s of (matrix bytes + activations + y) with T = 4 and T = 1 activation columns. Enough distinct
     matrices are cycled that no launch finds its weights in the 256 MB MALL (as in a decode step, which streams
-    all 64 layers' weights)."""
+    all 64 layers' weights); the launches are replayed from one HIP graph whose nodes walk the matrices, as a decode
+    step's graph issues them (launched one by one from Python, launches of up to about 10 us measured the host's
+    launch rate; in the graph each figure includes the node's own cost, about 1.5 us)."""
     import math
 
     dev = torch.device("cuda:0")
@@ -537,7 +539,8 @@ def bench_gemv(q27, torch):
                 xq = torch.randint(-127, 128, (nc * K,), dtype=torch.int8, device=dev, generator=g)
                 xd = torch.rand(nc * K // 32, device=dev, generator=g) * 0.01
                 y = torch.empty(nc * N, device=dev)
-                us = time_back_to_back(torch, lambda i: q27.ops.qgemv(mats[i % cnt], xq, xd, y, nc), 3 * cnt)
+                it = iter(range(1 << 30))  # the graph's nodes walk the matrices
+                us = time_graph(torch, lambda: (lambda i: q27.ops.qgemv(mats[i % cnt], xq, xd, y, nc))(next(it)), cnt)
                 b = nbytes + nc * K * (1 + 4 / 32) + nc * N * 4
                 res[f"{N}x{K}_T{nc}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
                                          "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 3), "matrix_MB": round(nbytes / 1e6, 2)}
@@ -827,6 +830,8 @@ def bench_decode_graph(q27, torch, replays):
 def bench_isolated(q27, torch, P, reps=3):
     """Every prefill op alone: all of its launches of the cold pass back to back between two HIP events (distinct
     inputs per launch, so the MALL does not serve them: 48-128 launches of 42-285 MB each), best of `reps` rounds.
+    Launched from the host (the shortest, the gather, takes 8.5 us on the GPU, above the host's launch interval; a
+    graph adds about 1.5 us per node here: 10.1 us).
     rmsnorm_q8 and the gather run once per pass; they are cycled over the 8 residual buffers instead."""
     o, M = q27.ops, P.M
     groups = {}
@@ -928,6 +933,7 @@ def main():
                     help="only the per-op isolated legs of the prefill pass (each op's launches back to back)")
     ap.add_argument("--gdn-only", action="store_true", help="only the delta-rule recurrence legs (for rocprof counter runs)")
     ap.add_argument("--wire-only", action="store_true", help="only the gemv_bf16_pair and two-card wire-format legs")
+    ap.add_argument("--gemv-only", action="store_true", help="only the decode GEMV legs (every weight type)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the fused-op path has no multi-GPU form in this build "
@@ -958,6 +964,9 @@ def main():
         return
     if args.gdn_only:
         print(json.dumps({"gdn_recurrence": bench_gdn(q27, torch)}), flush=True)
+        return
+    if args.gemv_only:
+        print(json.dumps({"decode_gemv": bench_gemv(q27, torch)}), flush=True)
         return
     if args.wire_only:
         print(json.dumps({"gemv_bf16_pair": bench_bf16_pair(q27, torch), "wire_formats": bench_wire(q27, torch)}),
