@@ -191,10 +191,14 @@ __global__ void __launch_bounds__(192) gdn_conv_decode_kernel(const float* __res
     const float* st = planes + ((size_t)pin * C + cb + 32 * k) * 3;
     in[0][k] = st[0]; in[1][k] = st[1]; in[2][k] = st[2];
   }
+  // rows past the batch are loaded from its last row (an address inside x) and never selected: token t's window
+  // reads rows <= t < T only. Unconditional loads and the register selects below keep the code free of per-lane
+  // branches (the conditional form compiled to a cascade of divergent branches, each waiting on its own loads).
 #pragma unroll
   for (int r = 0; r < 4; r++) {
+    const int rr = r < T ? r : T - 1;
 #pragma unroll
-    for (int k = 0; k < 4; k++) in[3 + r][k] = (r < T && r <= t) ? x[(size_t)r * C + cb + 32 * k] : 0.0f;
+    for (int k = 0; k < 4; k++) in[3 + r][k] = x[(size_t)rr * C + cb + 32 * k];
   }
   float w[4][4];
 #pragma unroll
@@ -202,14 +206,20 @@ __global__ void __launch_bounds__(192) gdn_conv_decode_kernel(const float* __res
     const float4 wv = ld4(cw + 4 * (size_t)(cb + 32 * k));
     w[k][0] = wv.x; w[k][1] = wv.y; w[k][2] = wv.z; w[k][3] = wv.w;
   }
-  // window of token t (registers, selected with constant indices)
+  // window of token t, picked by the two bits of t (selects; a chain of t == c tests becomes a switch, i.e.
+  // branches that split the wave)
+  const bool b0 = (t & 1) != 0, b1 = (t & 2) != 0;
+  auto pick = [&](float a0, float a1, float a2, float a3) {
+    const float lo = b0 ? a1 : a0, hi = b0 ? a3 : a2;
+    return b1 ? hi : lo;
+  };
   float s0[4], s1[4], s2[4], xn[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    s0[k] = t == 0 ? in[0][k] : t == 1 ? in[1][k] : t == 2 ? in[2][k] : in[3][k];
-    s1[k] = t == 0 ? in[1][k] : t == 1 ? in[2][k] : t == 2 ? in[3][k] : in[4][k];
-    s2[k] = t == 0 ? in[2][k] : t == 1 ? in[3][k] : t == 2 ? in[4][k] : in[5][k];
-    xn[k] = t == 0 ? in[3][k] : t == 1 ? in[4][k] : t == 2 ? in[5][k] : in[6][k];
+    s0[k] = pick(in[0][k], in[1][k], in[2][k], in[3][k]);
+    s1[k] = pick(in[1][k], in[2][k], in[3][k], in[4][k]);
+    s2[k] = pick(in[2][k], in[3][k], in[4][k], in[5][k]);
+    xn[k] = pick(in[3][k], in[4][k], in[5][k], in[6][k]);
   }
   __syncthreads();  // every plane read of the workgroup is consumed before any snapshot write
   if (!active) return;
