@@ -86,6 +86,10 @@ FAKE = 1 << 20  # an aligned non-null address: the calls below must fail before 
     (lambda o: o.get_rows_q8_0(FAKE, 100, FAKE, 4, FAKE, 5120, 0), -1, "row_bytes"),
     (lambda o: o.rmsnorm_q8(FAKE + 4, FAKE, None, FAKE, FAKE, 5120, 4, 1e-6, 0), -4, "alignment"),
     (lambda o: o.attn_prep(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 1e-6, 0.6, 24, 4, 0, True, 0), -1, "bad shape"),
+    (lambda o: o.gemv_bf16_pair(FAKE, FAKE, FAKE, FAKE, FAKE, 48, 5121, 4, 0), -1, "K % 8"),
+    (lambda o: o.gemv_bf16_pair(FAKE, FAKE + 2, FAKE, FAKE, FAKE, 48, 5120, 4, 0), -4, "alignment"),
+    (lambda o: o.gemv_bf16_pair(FAKE, FAKE, None, FAKE, FAKE, 48, 5120, 4, 0), -4, "null pointer"),
+    (lambda o: o.gated_rmsnorm_q8(FAKE + 4, FAKE, FAKE, FAKE, FAKE, 48, 1e-6, 0), -4, "alignment"),
 ])
 def test_rejected_before_launch(q27, call, code, needle):
     with pytest.raises(q27.Q27Error) as ei:
