@@ -74,8 +74,9 @@ inline void gdn_step(const float* q, const float* k, const float* v, int stride,
                            flip ? 1 : 0));
 }
 // No counterpart in the reference: the GDN prefill path bit-exact against the checker (true: gdn_step's prefill
-// sequential, gdn_conv_prefill's SiLU correctly rounded) or the faster forms within float32 rounding (false, the
-// default: the chunked recurrence on matrix cores from 128 tokens on, the hardware-exp SiLU), process-wide; returns
+// sequential, gdn_conv_prefill's SiLU and L2 scale correctly rounded) or the faster forms within the 1e-5 fp32 bar
+// (false, the default: the chunked recurrence on matrix cores from 128 tokens on, the hardware-exp SiLU and rsq L2
+// scale of the conv), process-wide; returns
 // the previous setting. Read when a gdn_step call
 // enqueues its launch, not at graph replay; threads that change it race with other threads' calls.
 inline bool gdn_prefill_exact(bool on) { return q27h_gdn_prefill_exact(on ? 1 : 0) != 0; }

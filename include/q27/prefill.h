@@ -5,7 +5,7 @@
 
 namespace q27 {
 
-// src/prefill.h:14-16. y's SiLU within float32 rounding unless gdn_prefill_exact(true) (q27/ops.h).
+// src/prefill.h:14-16. y within 4.1e-6 relative (hardware exp2 / rcp / rsq) unless gdn_prefill_exact(true) (q27/ops.h).
 inline void gdn_conv_prefill(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int M,
                              int n_norm_heads, float eps, const float* a, const float* b, const float* ssm_a,
                              const float* dt_bias, float* g, float* beta, int H, hipStream_t s) {

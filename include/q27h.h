@@ -120,8 +120,8 @@ int q27h_gdn_step_chunked(const float* q, const float* k, const float* v, int st
                           float scale, q27h_stream_t s);
 /* Process-wide choice for the Gated-DeltaNet prefill path: 1 = the CPU checker's bits (gdn_step's prefill (flip)
  * mode always on the sequential kernel, gdn_conv_prefill's SiLU correctly rounded), 0 (the default) = the faster
- * forms within float32 rounding (the chunked recurrence from 128 tokens on, the hardware-exp SiLU in
- * gdn_conv_prefill). Returns the previous setting. No counterpart
+ * forms within the fp32 tolerance of 1e-5 relative (the chunked recurrence from 128 tokens on, the hardware
+ * exp2 / reciprocal SiLU and rsq L2 scale in gdn_conv_prefill). Returns the previous setting. No counterpart
  * in the reference (its prefill is sequential); for callers that need the sequential bits. The setting is read when
  * q27h_gdn_step enqueues its launch: a graph captured under one setting keeps that path at every replay, and a thread
  * that changes it races with other threads' calls (a caller that needs a fixed path can call
@@ -133,9 +133,10 @@ int q27h_gdn_conv_l2(const float* x, const float* w, float* planes, const int* i
                      int snapshots, int n_norm_heads, float eps, const float* a, const float* b, const float* ssm_a,
                      const float* dt_bias, float* g, float* beta, int H, q27h_stream_t s, const void* pf, size_t pf_bytes);
 /* gdn_conv_prefill (src/prefill.h:14-16, src/prefill.cu:479-485): the same over M tokens; the conv state after
- * the batch goes to plane (*in_plane == 0 ? 1 : 0). y's SiLU is evaluated within float32 rounding (relative error
- * below 1e-6 where |y| is normal), not bit for bit, unless q27h_gdn_prefill_exact(1) was called; the state planes,
- * g and beta are bit-exact either way. */
+ * the batch goes to plane (*in_plane == 0 ? 1 : 0). y's SiLU and the q / k heads' L2 scale are evaluated on the
+ * hardware exp2, reciprocal and reciprocal square root (relative error below 4.1e-6 where |y| is normal, under the
+ * 1e-5 fp32 bar), not bit for bit, unless q27h_gdn_prefill_exact(1) was called; the state planes, g and beta are
+ * bit-exact either way. */
 int q27h_gdn_conv_prefill(const float* x, const float* w, float* planes, const int* in_plane, float* y, int C, int M,
                           int n_norm_heads, float eps, const float* a, const float* b, const float* ssm_a,
                           const float* dt_bias, float* g, float* beta, int H, q27h_stream_t s);

@@ -33,6 +33,14 @@ __device__ __forceinline__ float conv4(float s0, float s1, float s2, float xn, c
 }
 
 // L2 norm of one 128-channel head held by a 32-lane half, out[k] = channel v + 32k of lane p (layout above).
+// Q27H_CONV_RSQ = 1 (the default): the prefill conv's tolerance mode takes the L2 scale from the hardware reciprocal
+// square root (within one ulp) instead of the correctly rounded 1 / sqrtf (a chain of about 26 instructions per token
+// on each lane of a normed head); measured together with the lean SiLU (Q27H_SILU_LEAN, q27h_device.h): 34.8-35.4
+// against 35.9-36.2 us per launch. The exact mode and the decode conv keep 1 / sqrtf.
+#ifndef Q27H_CONV_RSQ
+#define Q27H_CONV_RSQ 1
+#endif
+template <bool RSQ = false>
 __device__ __forceinline__ void l2_head_lanes(float (&out)[4], float eps) {
   float acc = 0.0f;
 #pragma unroll
@@ -42,7 +50,8 @@ __device__ __forceinline__ void l2_head_lanes(float (&out)[4], float eps) {
   acc += lane_xor<7>(acc);
   acc += lane_xor<2>(acc);
   acc += lane_xor<1>(acc);
-  const float scale = 1.0f / __builtin_sqrtf(acc / 128.0f + eps / 128.0f);
+  const float scale = RSQ ? __builtin_amdgcn_rsqf(acc / 128.0f + eps / 128.0f)
+                          : 1.0f / __builtin_sqrtf(acc / 128.0f + eps / 128.0f);
   const float post = 1.0f / __builtin_sqrtf(128.0f);
 #pragma unroll
   for (int k = 0; k < 4; k++) out[k] = (out[k] * scale) * post;
@@ -70,10 +79,11 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
 // slower: 41-54 against 37.4 us at M = 2048. Spans of 4 tokens (64 VGPRs, 8 waves per SIMD) measured 37.2 us against
 // 39.2 / 37.3 / 37.9 us for spans of 3 / 5 / 8 and 10.43-10.46 against 10.47-10.54 ms per prefill pass for 8; the
 // token loop without a branch per token (the out-of-range silu redone after the stores) measured the same (37.1 us).
-// FAST: the SiLU in silu_tol (hardware exp2 and reciprocal, a Newton step; within a few float32 ulps instead of the
-// checker's bits): 35.6-36.0 against 37.3-37.4 us at M = 2048, and 40-50 us less per prefill pass; the same kernel
-// with no SiLU at all ran 34.7-35.0 us, so what remains above a copy of its access shape is the conv, the L2 norm
-// and the stream itself.
+// FAST: the SiLU on the hardware exp2 and reciprocal (q27_silu_tol_n) and the L2 scale on the hardware rsq, within
+// the north_star's fp32 tolerance instead of the checker's bits. The SiLU with a rounding term and a Newton step
+// (silu_tol, a few ulps) measured 35.6-36.0 against 37.3-37.4 us for the exact one at M = 2048; without both
+// refinements and with the rsq scale 34.8-35.4 against 35.9-36.2 us. The same kernel with no SiLU at all ran
+// 34.7-35.0 us, so what remains above a copy of its access shape is the conv, the L2 norm and the stream itself.
 template <int SPAN, bool FAST>
 __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __restrict__ x, const float* __restrict__ cw,
                                                                float* __restrict__ planes, const int* __restrict__ in_plane,
@@ -147,7 +157,7 @@ __global__ void __launch_bounds__(256) gdn_conv_prefill_kernel(const float* __re
     }
     if constexpr (FAST) q27_silu_tol_n(cv, cur);
     else q27_silu_n(cv, cur);
-    if (norm) l2_head_lanes(cur, eps);
+    if (norm) l2_head_lanes<FAST && Q27H_CONV_RSQ>(cur, eps);
     float* yr = y + (size_t)t * C + cb;
 #pragma unroll
     for (int k = 0; k < 4; k++) st_f32<kGdnNT>(yr + 32 * k, cur[k]);
@@ -353,7 +363,7 @@ extern "C" int q27h_gdn_conv_prefill(const float* x, const float* w, float* plan
   const int gate_blocks = (int)(((long)M * H + 255) / 256);
   const int nspans = (M + span - 1) / span;
   const long tiles = ((long)((C / 128 + 7) / 8) * nspans + 7) / 8 * 8;  // a whole number of tiles per XCD
-  // the SiLU of the conv output: within float32 rounding (silu_tol) unless the process asked for the checker's bits
+  // the SiLU and L2 scale of the conv output: within the fp32 tolerance unless the process asked for the checker's bits
   // (q27h_gdn_prefill_exact, read here when the launch is enqueued)
   if (gdn_prefill_exact_mode())
     hipLaunchKernelGGL((gdn_conv_prefill_kernel<span, false>), dim3((unsigned)(tiles + gate_blocks)), dim3(256), 0,

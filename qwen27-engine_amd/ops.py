@@ -85,8 +85,9 @@ def gdn_step_chunked(q, k, v, stride, g, beta, planes, in_plane, o, H, HK, T, sc
 
 def gdn_prefill_exact(on):
     """Process-wide: True = the GDN prefill path in the checker's bits (gdn_step's prefill sequential,
-    gdn_conv_prefill's SiLU correctly rounded), False (the default) = the faster forms within float32 rounding (the
-    chunked recurrence from 128 tokens on, the hardware-exp SiLU). Returns the previous setting."""
+    gdn_conv_prefill's SiLU and L2 scale correctly rounded), False (the default) = the faster forms within the 1e-5
+    fp32 bar (the chunked recurrence from 128 tokens on, the hardware-exp SiLU and rsq L2 scale of the conv). Returns
+    the previous setting."""
     return bool(lib().q27h_gdn_prefill_exact(int(bool(on))))
 
 

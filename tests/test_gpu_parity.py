@@ -384,7 +384,10 @@ def test_gdn_conv_prefill_default_tolerance(q27, oracle, T, M, pin, xscale):
     say(f"  max relative error {rel:.2e}; values differing from the checker's bits: "
         f"{np.count_nonzero(got[0].view(np.uint32) != oy.view(np.uint32))} of {oy.size}")
     assert rel <= SILU_RTOL
-    assert np.all(np.abs(y[~big]) <= SILU_TINY)
+    # values under the floor stay under it, up to the relative tolerance at its edge
+    off = np.flatnonzero(~big & (np.abs(y) > SILU_TINY * (1 + SILU_RTOL)))
+    assert off.size == 0, f"tiny values: {off.size}, first (index, got, want): " + str(
+        [(int(i), float(y[i]), float(w[i])) for i in off[:5]])
     for g_, w_, what in zip(got[1:], (ost, og, ob), ("planes", "g", "beta")):
         assert_bits_equal(g_, w_, what)
 
