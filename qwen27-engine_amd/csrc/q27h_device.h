@@ -179,19 +179,20 @@ __device__ __forceinline__ float q27_expf(float x) {
   return x != x ? x + x : e;
 }
 
-// n / d, correctly rounded, for 2^-60 <= |n| <= 2^7 and 1 <= d <= 2^87. This is gfx9's IEEE division sequence
-// (reciprocal, one Newton step, quotient, two residual corrections) without its range scaling and special-case
-// fix-up, which leave every operand unchanged in this range (no operand, residual or quotient comes near the
-// subnormal or overflow range), so the result is bit-identical to n / d.
-__device__ __forceinline__ float div_in_range(float n, float d) {
+// x / d for silu's operands, correctly rounded: d = 1 + q27_expf_core(-x) with 2^-60 <= |x| <= 60. The steps of gfx9's
+// IEEE division sequence (reciprocal, one Newton step, quotient, residual correction) without its range scaling and
+// fix-up, which leave every operand unchanged here, and with one residual correction instead of two: over every
+// float x of that range (3.3e9 cases with the hardware reciprocal modelled as the correctly rounded one moved by -1, 0
+// or +1 ulp; tests/test_device_silu_div.py) the one-correction quotient equals the two-correction one and x / d. The
+// single exception, shared by both sequences, is x = 2^-23 (d = 2 - 2^-23) with a reciprocal one ulp off; the GPU
+// test of silu covers that argument on the hardware.
+__device__ __forceinline__ float div_silu(float x, float d) {
   const float y0 = __builtin_amdgcn_rcpf(d);
   const float e = __builtin_fmaf(-d, y0, 1.0f);
   const float y = __builtin_fmaf(e, y0, y0);
-  const float q0 = n * y;
-  const float r0 = __builtin_fmaf(-d, q0, n);
-  const float q1 = __builtin_fmaf(r0, y, q0);
-  const float r1 = __builtin_fmaf(-d, q1, n);
-  return __builtin_fmaf(r1, y, q1);
+  const float q0 = x * y;
+  const float r0 = __builtin_fmaf(-d, q0, x);
+  return __builtin_fmaf(r0, y, q0);
 }
 
 // log for the softplus gate: x = 2^e m, m in [sqrt(1/2), sqrt(2)), s = f / (2 + f), log m = 2 atanh(s) as an
@@ -221,22 +222,22 @@ __device__ __forceinline__ float q27_logf(float x) {
   return __builtin_fmaf(fe, 0.693145752f, __builtin_fmaf(fe, 1.42860677e-06f, logm));
 }
 
-// silu(x) = x / (1 + e^-x). For 2^-60 <= |x| <= 60 the exp needs no clamp and the division is in div_in_range's
-// range (1 + e^-x <= 2^87); other arguments (zeros, subnormals, large or non-finite values) take the general path.
+// silu(x) = x / (1 + e^-x). For 2^-60 <= |x| <= 60 the exp needs no clamp and the division is div_silu's
+// (1 + e^-x <= 2^87); other arguments (zeros, subnormals, large or non-finite values) take the general path.
 __device__ __forceinline__ float q27_silu(float x) { return x / (1.0f + q27_expf(-x)); }
 __device__ __forceinline__ bool silu_fast_ok(float x) {
   const float ax = __builtin_fabsf(x);
   return ax >= 0x1p-60f && ax <= 60.0f;
 }
 // silu on the fast range only (2^-60 <= |x| <= 60, see silu_fast_ok); equal to q27_silu there.
-__device__ __forceinline__ float silu_fast(float x) { return div_in_range(x, 1.0f + q27_expf_core(-x)); }
+__device__ __forceinline__ float silu_fast(float x) { return div_silu(x, 1.0f + q27_expf_core(-x)); }
 // N values at once, one branch for the lanes with an argument outside the fast range.
 template <int N>
 __device__ __forceinline__ void q27_silu_n(const float (&x)[N], float (&out)[N]) {
   bool ok = true;
 #pragma unroll
   for (int k = 0; k < N; k++) {
-    out[k] = div_in_range(x[k], 1.0f + q27_expf_core(-x[k]));
+    out[k] = div_silu(x[k], 1.0f + q27_expf_core(-x[k]));
     ok &= silu_fast_ok(x[k]);
   }
   if (!ok) {

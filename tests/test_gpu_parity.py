@@ -237,13 +237,14 @@ def test_gated_rmsnorm_q8(q27, oracle, T, heads):
 # ---------------------------------------------------------------- silu over a sweep of float32 bit patterns
 def test_silu_bit_pattern_sweep(q27, oracle, T):
     """silu(g) * 1 through the unfused swiglu: every 61st float32 bit pattern (about 70 million values: both
-    signs, subnormals, zeros, infinities), plus the neighbours of the fast range's edges 2^-60 and 60. The
+    signs, subnormals, zeros, infinities), plus the neighbours of the fast range's edges 2^-60 and 60 and of 2^-23 (the
+    one argument whose quotient depends on the hardware reciprocal of 2 - 2^-23 being correctly rounded). The
     kernels compute silu with a division without range scaling for 2^-60 <= |x| <= 60 and the general one elsewhere; both
     must give the oracle's bits. NaN inputs and outputs only have to be NaN (payloads are not specified)."""
     say("silu bit-pattern sweep")
     pats = np.arange(0, 1 << 32, 61, dtype=np.uint64).astype(np.uint32)
     edges = []
-    for e in (np.float32(2.0 ** -60), np.float32(60.0)):
+    for e in (np.float32(2.0 ** -60), np.float32(60.0), np.float32(2.0 ** -23)):
         b = int(np.array(e).view(np.uint32))
         edges += list(range(b - 64, b + 65))
     edges = np.array(edges, np.uint32)
