@@ -80,7 +80,7 @@ __device__ __forceinline__ void gate_one(const float* __restrict__ a, const floa
 // 39.2 / 37.3 / 37.9 us for spans of 3 / 5 / 8 and 10.43-10.46 against 10.47-10.54 ms per prefill pass for 8; the
 // token loop without a branch per token (the out-of-range silu redone after the stores) measured the same (37.1 us).
 // FAST: the SiLU on the hardware exp2 and reciprocal (q27_silu_tol_n) and the L2 scale on the hardware rsq, within
-// the north_star's fp32 tolerance instead of the checker's bits. The SiLU with a rounding term and a Newton step
+// the path's fp32 tolerance (1e-5 relative) instead of the checker's bits. The SiLU with a rounding term and a Newton step
 // (silu_tol, a few ulps) measured 35.6-36.0 against 37.3-37.4 us for the exact one at M = 2048; without both
 // refinements and with the rsq scale 34.8-35.4 against 35.9-36.2 us. The same kernel with no SiLU at all ran
 // 34.7-35.0 us, so what remains above a copy of its access shape is the conv, the L2 norm and the stream itself.

@@ -269,7 +269,7 @@ __device__ __forceinline__ float silu_tol(float x) {
 #endif
 // silu_tol without the product's rounding term and the Newton step: e = 2^(-|x| log2 e) on the hardware exp2 (the
 // argument's rounding moves e by up to |x| 2^-24 relative), the hardware reciprocal of 1 + e. Relative error below
-// 4.1e-6 on [-87, 87] with both hardware operations off by one ulp (the north_star's fp32 bar is 1e-5); the error
+// 4.1e-6 on [-87, 87] with both hardware operations off by one ulp (the fp32 tolerance of the path is 1e-5); the error
 // profile of an exp2-based expf and an approximate reciprocal, as a fast-math build of the reference computes silu.
 __device__ __forceinline__ float silu_lean(float x) {
   const float e = __builtin_amdgcn_exp2f(__builtin_fabsf(x) * -1.44269502f);
